@@ -1,0 +1,188 @@
+"""Benchmark: snapjudge encoder forward on one MI355X.
+
+Workload: the 22-layer / hidden 768 / 12x64 heads /
+GEGLU 1152 / vocab 50368 ModernBERT-style DecisionModel encoder with
+random N(0, 0.02) bf16 weights (seed 0), batch 64 x seq 512, row lengths
+~ U[64, 512] (seed 1), right-padded.  One step = one encoder forward
+(DecisionModel::encode, src/model.cpp:222-307) over the batch, with the token
+ids already resident in HBM (sjh_model_encode_device).
+
+value = valid (non-pad) encoder tokens per second.  Also reported:
+  roofline      -- the dominant kernel (the bf16 MFMA projection GEMM that
+                   serves QKV+RoPE, Wo+residual, Wi+GEGLU, Wo2+residual):
+                   algorithmic FLOPs per launch / mean launch time, measured
+                   with hipEvents on the model's stream over a profiled
+                   repeat of the timed steps;
+  attention_mfma_frac -- the attention kernel's algorithmic FLOPs
+                   (4*D*sum(n^2) per layer) over its time, vs bf16 peak;
+  p50_latency_b1_ms -- config 2 (batch 1, seq 128, no padding) encoder
+                   latency, hipGraph replay, p50 of 50;
+  cpu_baseline  -- the reference's own CPU forward (oracle/_ref, compiled
+                   from its sources, no-BLAS build) on a bounded sample of the
+                   same workload, extrapolated by layers.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "encoder tokens/sec at B64×S512 bf16 (1 GPU); attention MFMA % peak; p50 latency at B1"
+PEAK_BF16_TFLOPS = 2500.0
+GEMM_NAMES = ("gemm_qkv_rope", "gemm_wo_resid", "gemm_wi_geglu", "gemm_wo2_resid")
+
+
+def gemm_flops_per_token(D, F, layers):
+    return 2.0 * layers * (3 * D * D + D * D + 2 * D * F + D * F)
+
+
+def cpu_baseline(w, rl, enc, ids, mask, lens, layers_full):
+    """Reference CPU encode on 4 rows (length quantiles of the batch) through
+    1 layer of the same model, extrapolated to all layers."""
+    from oracle import RefModel
+    from snapjudge_amd import synth
+
+    if not RefModel.available():
+        return None
+    keep = {k: v for k, v in w.items()
+            if not k.startswith("encoder.layers.") or k.startswith("encoder.layers.0.")}
+    enc1 = dict(enc, num_hidden_layers=1, layer_types=enc["layer_types"][:1])
+    order = np.argsort(lens)
+    rows = [order[int(q * (len(lens) - 1))] for q in (0.2, 0.4, 0.6, 0.8)]
+    os.environ["SNAPJUDGE_THREADS"] = "1"
+    with tempfile.TemporaryDirectory() as d:
+        synth.write_checkpoint(d, rl, enc1, keep, store="BF16")
+        ref = RefModel(d)
+        ntok, secs = 0, 0.0
+        for b in rows:
+            n = int(lens[b])
+            t0 = time.perf_counter()
+            ref.encode(ids[b:b + 1, :n], mask[b:b + 1, :n])
+            secs += time.perf_counter() - t0
+            ntok += n
+    tps = ntok / (secs * layers_full)
+    return {"value": round(tps, 2), "unit": "tokens/s", "cores": 1, "kind": "reference",
+            "sample": f"reference DecisionModel::encode (no-BLAS build, SNAPJUDGE_THREADS=1) on "
+                      f"{len(rows)} rows of the batch (sum n = {ntok}) through 1 of "
+                      f"{layers_full} layers: {secs:.1f} s, extrapolated x{layers_full}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only; the encoder shards across GPUs by "
+              "sequence with no exchange (see DESIGN.md) but no multi-GPU path is built.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import snapjudge_amd as sj
+    from snapjudge_amd import synth
+
+    B, S, LO, HI = 64, 512, 64, 512
+    p = synth.PRESETS["cfg3"]
+    rl, enc, w = synth.make_model(**p, seed=0)
+    cfg = synth.flat_cfg(rl, enc)
+    D, F, NL, H = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"], cfg["num_attention_heads"]
+    ids, mask, lens = synth.make_batch(B, S, LO, HI, cfg["vocab_size"], seed=1)
+    T = int(lens.sum())
+
+    model = sj.Model(w, cfg, precision=sj.SJH_PREC_BF16, use_graphs=True)
+    packed = np.concatenate([ids[b, :lens[b]] for b in range(B)]).astype(np.int32)
+    d_ids = torch.from_numpy(packed).cuda()
+    d_out = torch.empty((T, D), dtype=torch.float32, device="cuda")
+    lens32 = lens.astype(np.int32)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        model.encode_device(d_ids.data_ptr(), lens32, d_out.data_ptr(), stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = T * args.steps / elapsed
+
+    # profiled repeat of the timed steps: hipEvents around every launch
+    model.profile(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    prof = model.profile_read()
+    model.profile(False)
+    gemm_ms = sum(prof[n][0] for n in GEMM_NAMES if n in prof)
+    gemm_launches = sum(prof[n][1] for n in GEMM_NAMES if n in prof)
+    gemm_flops_step = gemm_flops_per_token(D, F, NL) * T
+    flops_per_launch = gemm_flops_step * args.steps / gemm_launches
+    avg_launch_s = gemm_ms / 1e3 / gemm_launches
+    achieved = flops_per_launch / avg_launch_s / 1e12
+    attn_ms, attn_n = prof.get("attention", (0.0, 0))
+    attn_flops_step = NL * 4.0 * D * float((lens.astype(np.float64) ** 2).sum())
+    attn_tflops = attn_flops_step * args.steps / (attn_ms / 1e3) / 1e12 if attn_ms else 0.0
+
+    # config 2: batch 1, seq 128, p50 latency (graph replay)
+    rng = np.random.default_rng(7)
+    ids2 = rng.integers(0, cfg["vocab_size"], size=128).astype(np.int32)
+    d_ids2 = torch.from_numpy(ids2).cuda()
+    d_out2 = torch.empty((128, D), dtype=torch.float32, device="cuda")
+    l2 = np.array([128], np.int32)
+    lat = []
+    for i in range(60):
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        model.encode_device(d_ids2.data_ptr(), l2, d_out2.data_ptr(), stream)
+        torch.cuda.synchronize()
+        if i >= 10:
+            lat.append((time.perf_counter() - t1) * 1e3)
+    p50 = float(np.median(lat))
+    model.close()
+
+    cpu = None if args.no_cpu else cpu_baseline(w, rl, enc, ids, mask, lens, NL)
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 3: 22-layer/768 ModernBERT-style encoder, "
+                               "bf16 weights N(0,0.02) seed 0, batch 64 x seq 512, "
+                               "lengths U[64,512] seed 1 (valid tokens only)",
+                   "global_batch": B, "seq_len": S, "valid_tokens_per_step": T,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "gemm_bf16_mfma_kernel (QKV+RoPE, Wo+res, Wi+GEGLU, Wo2+res)",
+                     "launches_per_step": gemm_launches // args.steps,
+                     "flops_per_launch": flops_per_launch,
+                     "avg_launch_us": round(avg_launch_s * 1e6, 3)},
+        "attention_mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+        "attention_tflops": round(attn_tflops, 2),
+        "p50_latency_b1_ms": round(p50, 4),
+        "padded_tokens_per_s": round(B * S * args.steps / elapsed, 1),
+        "kernel_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in sorted(prof.items())},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,190 @@
+/*
+ * snapjudge_hip.h -- C ABI of the MI355X (gfx950) encoder forward.
+ *
+ * Drop-in boundary for the reference's GPU fast-path hook.  Two layers:
+ *
+ *  1. Model level (replaces FastSnapjudge, include/snapjudge/fast.hpp:15-31 of
+ *     the reference): stage a DecisionModel's weights on the GPU once, then run
+ *     DecisionModel::forward (src/model.cpp:309-536) or ::encode
+ *     (src/model.cpp:222-307) on host-side [B][L] batches with exactly the
+ *     reference's argument meaning.
+ *
+ *  2. Kernel level (replaces the extern "C" launchers of cuda/kernels.cu,
+ *     bound by cuda/fast.cpp:23-34): GEMM with epilogues, GEGLU, residual +
+ *     LayerNorm, RoPE, attention, taking device pointers and a hipStream_t.
+ *
+ * Conventions (mirroring the reference engine ABI, include/snapjudge/capi.h):
+ * every entry point returns 0 on success or a negative SJH_E_* code; the
+ * message of the last failure on the calling thread is sjh_last_error().
+ * bf16 tensors are passed as raw 16-bit storage (uint16_t / void*).  Nothing
+ * here falls back to the CPU: without a usable gfx950 device, calls fail.
+ */
+#ifndef SNAPJUDGE_HIP_H
+#define SNAPJUDGE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* sjh_stream_t; /* == hipStream_t */
+
+enum {
+  SJH_OK = 0,
+  SJH_E_INVALID = -1, /* bad argument or shape */
+  SJH_E_DEVICE = -2,  /* HIP runtime error or no gfx950 device */
+  SJH_E_OOM = -3      /* device allocation failed */
+};
+
+enum { SJH_F32 = 0, SJH_BF16 = 1 }; /* element types */
+
+/* Numerics mode of a model.
+ *  SJH_PREC_FP32: fp32 weights and activations, fp32 accumulation
+ *                 (parity mode: hidden states within 1e-4 of the reference).
+ *  SJH_PREC_BF16: bf16 weights and activations, fp32 accumulation, fp32
+ *                 residual stream and LayerNorm statistics (within 2e-2). */
+enum { SJH_PREC_FP32 = 0, SJH_PREC_BF16 = 1 };
+
+/* One encoder layer: the reference's LayerWeights (include/snapjudge/model.hpp:37-44),
+ * fp32 host arrays, row-major, PyTorch Linear layout [out, in]. */
+typedef struct sjh_layer_desc {
+  const float* attn_norm; /* [D] or NULL (layer 0 has none, src/model.cpp:112-117) */
+  const float* wqkv;      /* [3D, D] */
+  const float* wo;        /* [D, D] */
+  const float* mlp_norm;  /* [D] */
+  const float* wi;        /* [2F, D]: rows [0,F) input half, [F,2F) gate half */
+  const float* wo2;       /* [D, F] */
+  int32_t window;         /* 0 = full attention, else local_attention/2 */
+  int32_t sliding;        /* 1 = use the sliding-attention RoPE tables */
+} sjh_layer_desc;
+
+/* One decision-head layer (src/model.cpp:107-111). */
+typedef struct sjh_head_desc {
+  const float *n1w, *n1b, *n2w, *n2b; /* [D] */
+  const float *in_w, *in_b;           /* [3D, D], [3D] */
+  const float *out_w, *out_b;         /* [D, D], [D] */
+  const float *l1w, *l1b;             /* [4D, D], [4D] */
+  const float *l2w, *l2b;             /* [D, 4D], [D] */
+} sjh_head_desc;
+
+/* Everything DecisionModel::forward reads (src/model.cpp:89-126). */
+typedef struct sjh_model_desc {
+  int32_t hidden_size, num_heads, intermediate_size, vocab_size, num_layers;
+  int32_t max_position; /* rows of the RoPE tables */
+  int32_t n_act, head_layers, lora_r;
+  float norm_eps;
+  double rope_theta_full, rope_theta_sliding; /* used when the tables below are NULL */
+  const float* emb_w;      /* [V, D] */
+  const float* emb_norm;   /* [D] */
+  const float* final_norm; /* [D] */
+  const float *rope_cos_full, *rope_sin_full;   /* [max_position, Dh/2] or NULL */
+  const float *rope_cos_slide, *rope_sin_slide; /* [max_position, Dh/2] or NULL */
+  const sjh_layer_desc* layers;                 /* [num_layers] */
+  const float* lora_a;   /* [r, D] or NULL */
+  const float* lora_b;   /* [D, r] or NULL */
+  const float* type_emb; /* [3, D] */
+  const sjh_head_desc* head; /* [head_layers] */
+  const float *sc_ln_w, *sc_ln_b; /* [D], [D] or NULL */
+  const float *sc_w1, *sc_b1;     /* [D, D], [D] or NULL */
+  const float *sc_w2, *sc_b2;     /* [1, D], [1] or NULL */
+  const float *act_w1, *act_b1;   /* [256, D+4], [256] */
+  const float *act_w2, *act_b2;   /* [n_act, 256], [n_act] */
+} sjh_model_desc;
+
+typedef struct sjh_options {
+  int32_t precision;  /* SJH_PREC_* */
+  int32_t max_len;    /* longest row accepted (the reference's max_len) */
+  int32_t use_graphs; /* replay the device work of a repeated batch shape as a hipGraph */
+  int32_t pad_rows;   /* 1: also compute padded query rows, as the reference does, so
+                         encode() returns its values at padded positions too; 0: work
+                         only on valid tokens (padded positions of encode() are 0) */
+  int32_t device;     /* HIP device ordinal */
+} sjh_options;
+
+typedef struct sjh_model sjh_model;
+
+const char* sjh_last_error(void);
+int sjh_version(void);
+void sjh_default_options(sjh_options* opt);
+
+/* FastSnapjudge::FastSnapjudge (cuda/fast.cpp:272-352): copies the weights to
+ * the device in the numerics mode's storage type.  The descriptor's arrays may
+ * be released after the call. */
+int sjh_model_create(const sjh_model_desc* desc, const sjh_options* opt, sjh_model** out);
+void sjh_model_destroy(sjh_model* m);
+
+/* DecisionModel::encode (src/model.cpp:222-307).  ids, mask: [B, L] int64,
+ * right-padded, mask 0/1.  hidden: [B, L, D] fp32, caller-allocated. */
+int sjh_model_encode(sjh_model* m, const int64_t* ids, const int64_t* mask, int32_t B, int32_t L,
+                     float* hidden);
+
+/* DecisionModel::forward (src/model.cpp:309-536) / FastSnapjudge::forward
+ * (cuda/fast.cpp:357-569).  marker_pos [B, K] int64, marker_mask [B, K] uint8,
+ * qtype [B] int64 in {0,1,2}.  logits [B, K] (masked = -1e4), act [B, n_act]. */
+int sjh_model_forward(sjh_model* m, const int64_t* ids, const int64_t* mask,
+                      const int64_t* marker_pos, const uint8_t* marker_mask, const int64_t* qtype,
+                      int32_t B, int32_t L, int32_t K, float* logits, float* act);
+
+/* Encoder on a batch already resident in device memory: d_ids [T] int32 holds
+ * the B sequences back to back, h_lens [B] (host) their lengths, T = sum.
+ * Writes the final hidden states [T, D] fp32 to d_hidden.  Work is enqueued on
+ * `stream` (NULL: the model's own stream); the call does not synchronize. */
+int sjh_model_encode_device(sjh_model* m, const int32_t* d_ids, const int32_t* h_lens, int32_t B,
+                            float* d_hidden, sjh_stream_t stream);
+
+/* Hidden size, heads, n_act and the precision a model was built with. */
+int sjh_model_info(const sjh_model* m, int32_t* D, int32_t* H, int32_t* n_act,
+                   int32_t* precision);
+
+/* Enable/disable per-kernel timing with hipEvents on the model's launches and
+ * read the totals: names[i] (static strings), total_ms[i], launches[i]. */
+int sjh_model_profile(sjh_model* m, int32_t enable);
+int sjh_model_profile_read(sjh_model* m, int32_t max_entries, const char** names,
+                           double* total_ms, int64_t* launches, int32_t* n_entries);
+
+/* ------------------------------------------------------------------------
+ * Kernel level.  All pointers are device pointers.
+ * ------------------------------------------------------------------------ */
+
+/* sj_gemm (cuda/kernels.cu:88-108): C[M,N] = act(A[M,K] . W[N,K]^T (+ bias)).
+ * act 0 none, 1 erf-GELU, 2 ReLU.  dtype applies to A, W and C; bias fp32 or NULL. */
+int sjh_gemm(const void* A, const void* W, const float* bias, void* C, int32_t M, int32_t N,
+             int32_t K, int32_t act, int32_t dtype, sjh_stream_t stream);
+
+/* sj_gemm_geglu (cuda/kernels.cu:168-174): C[M,F] = gelu(A.Wi[:F]^T) * (A.Wi[F:]^T),
+ * Wi [2F, K]. */
+int sjh_gemm_geglu(const void* A, const void* Wi, void* C, int32_t M, int32_t F, int32_t K,
+                   int32_t dtype, sjh_stream_t stream);
+
+/* X[M,D] (fp32) += C[M,N=D] where C = A[M,K] . W[D,K]^T: the residual-add
+ * epilogue that the reference runs as gemm + add_ (src/model.cpp:389-391). */
+int sjh_gemm_residual(const void* A, const void* W, float* X, int32_t M, int32_t D, int32_t K,
+                      int32_t dtype, sjh_stream_t stream);
+
+/* sj_add_ln (cuda/kernels.cu:243-254): if residual, X += R (R of dtype);
+ * Y = LN(X) * W (+ B if bias), Y of dtype.  X fp32 [M, D]. */
+int sjh_add_ln(float* X, const void* R, const float* W, const float* B, void* Y, int32_t M,
+               int32_t D, float eps, int32_t residual, int32_t bias, int32_t dtype,
+               sjh_stream_t stream);
+
+/* sj_rope (cuda/kernels.cu:282-288): in-place rotate-half on packed qkv
+ * [M, 3*H*Dh], row r at position r % L; cos/sin fp32 [L_max, Dh/2]. */
+int sjh_rope(void* qkv, const float* cos_t, const float* sin_t, int64_t M, int32_t L, int32_t H,
+             int32_t Dh, int32_t dtype, sjh_stream_t stream);
+
+/* sj_attn (cuda/kernels.cu:351-357): qkv [B, L, 3, H, Dh], lens [B] int32 ->
+ * O [B, L, H*Dh]; every query row of each sequence attends to its first
+ * lens[b] keys (window > 0: |i-j| <= window).  dtype applies to qkv and O. */
+int sjh_attn(const void* qkv, const int32_t* lens, void* O, int32_t B, int32_t L, int32_t H,
+             int32_t Dh, int32_t window, int32_t dtype, sjh_stream_t stream);
+
+/* Embedding gather + LayerNorm (src/model.cpp:332-340): X[r] = LN(table[ids[r]]) * w.
+ * table [V, D] of dtype, ids int32 [M], X fp32 [M, D]. */
+int sjh_embed_ln(const void* table, const int32_t* ids, const float* w, float* X, int32_t M,
+                 int32_t D, float eps, int32_t dtype, sjh_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SNAPJUDGE_HIP_H */

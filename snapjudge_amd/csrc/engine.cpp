@@ -1,0 +1,1026 @@
+// engine.cpp -- device-resident DecisionModel forward (host orchestration).
+#include "engine.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "sjh_host.hpp"
+
+namespace sjh {
+
+// ------------------------------------------------------------------ buffers --
+DevBuf::~DevBuf() {
+  if (p_) (void)hipFree(p_);
+}
+
+DevBuf& DevBuf::operator=(DevBuf&& o) noexcept {
+  if (this != &o) {
+    if (p_) (void)hipFree(p_);
+    p_ = o.p_;
+    bytes_ = o.bytes_;
+    o.p_ = nullptr;
+    o.bytes_ = 0;
+  }
+  return *this;
+}
+
+void DevBuf::alloc(size_t bytes) {
+  if (p_) hip_check(hipFree(p_), "hipFree");
+  p_ = nullptr;
+  bytes_ = 0;
+  if (bytes == 0) return;
+  hipError_t e = hipMalloc(&p_, bytes);
+  if (e != hipSuccess) {
+    p_ = nullptr;
+    (void)hipGetLastError();
+    throw std::runtime_error("snapjudge HIP: out of device memory (" + std::to_string(bytes) +
+                             " bytes)");
+  }
+  bytes_ = bytes;
+}
+
+void DevBuf::ensure(size_t bytes) {
+  if (bytes > bytes_) alloc(bytes);
+}
+
+PinnedBuf::~PinnedBuf() {
+  if (p_) (void)hipHostFree(p_);
+}
+
+void PinnedBuf::ensure(size_t bytes) {
+  if (bytes <= bytes_) return;
+  if (p_) hip_check(hipHostFree(p_), "hipHostFree");
+  p_ = nullptr;
+  bytes_ = 0;
+  hip_check(hipHostMalloc(&p_, bytes, hipHostMallocDefault), "hipHostMalloc");
+  bytes_ = bytes;
+}
+
+namespace {
+
+uint16_t bf16_rne(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+DevBuf upload_f32(const float* src, size_t n, const char* what) {
+  if (!src) fail(std::string("model descriptor: missing ") + what);
+  DevBuf b;
+  b.alloc(n * sizeof(float));
+  hip_check(hipMemcpy(b.get(), src, n * sizeof(float), hipMemcpyHostToDevice), what);
+  return b;
+}
+
+DevBuf upload_bf16(const float* src, size_t n, const char* what) {
+  if (!src) fail(std::string("model descriptor: missing ") + what);
+  std::vector<uint16_t> tmp(n);
+  for (size_t i = 0; i < n; ++i) tmp[i] = bf16_rne(src[i]);
+  DevBuf b;
+  b.alloc(n * sizeof(uint16_t));
+  hip_check(hipMemcpy(b.get(), tmp.data(), n * sizeof(uint16_t), hipMemcpyHostToDevice), what);
+  return b;
+}
+
+DevBuf upload_opt_f32(const float* src, size_t n, const char* what) {
+  return src ? upload_f32(src, n, what) : DevBuf();
+}
+
+// RoPE tables exactly as src/model.cpp:173-190: inverse frequency and angle in
+// double, cos/sin rounded to float; [max_pos, Dh/2].
+void rope_table(double theta, int max_pos, int Dh, std::vector<float>& c, std::vector<float>& s) {
+  const int half = Dh / 2;
+  c.resize(static_cast<size_t>(max_pos) * half);
+  s.resize(c.size());
+  for (int pos = 0; pos < max_pos; ++pos)
+    for (int d = 0; d < half; ++d) {
+      const double inv = 1.0 / std::pow(theta, 2.0 * static_cast<double>(d) / Dh);
+      const double fr = static_cast<double>(pos) * inv;
+      c[static_cast<size_t>(pos) * half + d] = static_cast<float>(std::cos(fr));
+      s[static_cast<size_t>(pos) * half + d] = static_cast<float>(std::sin(fr));
+    }
+}
+
+size_t dt_size(int dt) { return dt == DT_BF16 ? 2 : 4; }
+
+template <typename T>
+const T* off(const void* base, int64_t elems, int dt) {
+  return reinterpret_cast<const T*>(static_cast<const char*>(base) + elems * dt_size(dt));
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ engine --
+Engine::Engine(const sjh_model_desc& d, const sjh_options& o) {
+  dev_ = o.device;
+  int ndev = 0;
+  hip_check(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+  if (dev_ < 0 || dev_ >= ndev) fail("device ordinal " + std::to_string(dev_) + " not present");
+  hip_check(hipSetDevice(dev_), "hipSetDevice");
+  hipDeviceProp_t prop;
+  hip_check(hipGetDeviceProperties(&prop, dev_), "hipGetDeviceProperties");
+  if (std::string(prop.gcnArchName).find("gfx950") == std::string::npos)
+    fail(std::string("device is ") + prop.gcnArchName + "; this library is built for gfx950");
+
+  require(o.precision == SJH_PREC_FP32 || o.precision == SJH_PREC_BF16, "unknown precision");
+  prec_ = o.precision;
+  act_dt_ = prec_ == SJH_PREC_BF16 ? DT_BF16 : DT_F32;
+  use_graphs_ = o.use_graphs != 0;
+  pad_rows_ = o.pad_rows != 0;
+
+  D_ = d.hidden_size;
+  H_ = d.num_heads;
+  F_ = d.intermediate_size;
+  V_ = d.vocab_size;
+  nlayers_ = d.num_layers;
+  max_pos_ = d.max_position;
+  n_act_ = d.n_act;
+  head_layers_ = d.head_layers;
+  lora_r_ = (d.lora_a && d.lora_b) ? d.lora_r : 0;
+  eps_ = d.norm_eps;
+  require(D_ > 0 && H_ > 0 && D_ % H_ == 0, "hidden_size must be a positive multiple of num_heads");
+  Dh_ = D_ / H_;
+  require(Dh_ % 2 == 0, "head_dim must be even");
+  require(F_ > 0 && V_ > 0 && nlayers_ > 0 && max_pos_ > 0, "bad model dimensions");
+  require(n_act_ > 0 && head_layers_ >= 0 && lora_r_ >= 0, "bad head dimensions");
+  require(d.layers != nullptr, "model descriptor: missing layers");
+  require(head_layers_ == 0 || d.head != nullptr, "model descriptor: missing head layers");
+  max_len_ = o.max_len > 0 ? std::min(o.max_len, max_pos_) : max_pos_;
+
+  hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  stage_weights(d);
+}
+
+Engine::~Engine() {
+  (void)hipSetDevice(dev_);
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  for (auto& kv : graphs_)
+    if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+  for (auto& p : prof_pending_) {
+    (void)hipEventDestroy(p.a);
+    (void)hipEventDestroy(p.b);
+  }
+  for (hipEvent_t e : ev_pool_) (void)hipEventDestroy(e);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Engine::stage_weights(const sjh_model_desc& d) {
+  const size_t D = D_, F = F_;
+  auto upload_w = [&](const float* p, size_t n, const char* what) {
+    return act_dt_ == DT_BF16 ? upload_bf16(p, n, what) : upload_f32(p, n, what);
+  };
+  emb_w_ = upload_w(d.emb_w, static_cast<size_t>(V_) * D, "emb_w");
+  emb_norm_ = upload_f32(d.emb_norm, D, "emb_norm");
+  final_norm_ = upload_f32(d.final_norm, D, "final_norm");
+
+  const size_t nt = static_cast<size_t>(max_pos_) * (Dh_ / 2);
+  std::vector<float> c, s;
+  if (d.rope_cos_full && d.rope_sin_full) {
+    rope_cos_full_ = upload_f32(d.rope_cos_full, nt, "rope_cos_full");
+    rope_sin_full_ = upload_f32(d.rope_sin_full, nt, "rope_sin_full");
+  } else {
+    rope_table(d.rope_theta_full, max_pos_, Dh_, c, s);
+    rope_cos_full_ = upload_f32(c.data(), nt, "rope_cos_full");
+    rope_sin_full_ = upload_f32(s.data(), nt, "rope_sin_full");
+  }
+  if (d.rope_cos_slide && d.rope_sin_slide) {
+    rope_cos_slide_ = upload_f32(d.rope_cos_slide, nt, "rope_cos_slide");
+    rope_sin_slide_ = upload_f32(d.rope_sin_slide, nt, "rope_sin_slide");
+  } else {
+    rope_table(d.rope_theta_sliding, max_pos_, Dh_, c, s);
+    rope_cos_slide_ = upload_f32(c.data(), nt, "rope_cos_slide");
+    rope_sin_slide_ = upload_f32(s.data(), nt, "rope_sin_slide");
+  }
+
+  layers_.resize(static_cast<size_t>(nlayers_));
+  for (int i = 0; i < nlayers_; ++i) {
+    const sjh_layer_desc& s0 = d.layers[i];
+    LayerDev& L = layers_[static_cast<size_t>(i)];
+    L.has_attn_norm = s0.attn_norm != nullptr;
+    if (L.has_attn_norm) L.attn_norm = upload_f32(s0.attn_norm, D, "attn_norm");
+    L.wqkv = upload_w(s0.wqkv, 3 * D * D, "wqkv");
+    L.wo = upload_w(s0.wo, D * D, "wo");
+    L.mlp_norm = upload_f32(s0.mlp_norm, D, "mlp_norm");
+    L.wi = upload_w(s0.wi, 2 * F * D, "wi");
+    L.wo2 = upload_w(s0.wo2, D * F, "wo2");
+    require(s0.window >= 0, "negative attention window");
+    L.window = s0.window;
+    L.sliding = s0.sliding;
+  }
+
+  if (lora_r_ > 0) {
+    lora_a_ = upload_f32(d.lora_a, static_cast<size_t>(lora_r_) * D, "lora_a");
+    lora_b_ = upload_f32(d.lora_b, D * static_cast<size_t>(lora_r_), "lora_b");
+  }
+  type_emb_ = upload_f32(d.type_emb, 3 * D, "type_emb");
+  head_.resize(static_cast<size_t>(head_layers_));
+  for (int i = 0; i < head_layers_; ++i) {
+    const sjh_head_desc& h = d.head[i];
+    HeadDev& hd = head_[static_cast<size_t>(i)];
+    hd.n1w = upload_f32(h.n1w, D, "head n1w");
+    hd.n1b = upload_f32(h.n1b, D, "head n1b");
+    hd.n2w = upload_f32(h.n2w, D, "head n2w");
+    hd.n2b = upload_f32(h.n2b, D, "head n2b");
+    hd.in_w = upload_w(h.in_w, 3 * D * D, "head in_w");
+    hd.in_b = upload_f32(h.in_b, 3 * D, "head in_b");
+    hd.out_w = upload_w(h.out_w, D * D, "head out_w");
+    hd.out_b = upload_f32(h.out_b, D, "head out_b");
+    hd.l1w = upload_w(h.l1w, 4 * D * D, "head l1w");
+    hd.l1b = upload_f32(h.l1b, 4 * D, "head l1b");
+    hd.l2w = upload_w(h.l2w, D * 4 * D, "head l2w");
+    hd.l2b = upload_f32(h.l2b, D, "head l2b");
+  }
+  sc_ln_w_ = upload_f32(d.sc_ln_w, D, "scorer ln weight");
+  sc_ln_b_ = upload_opt_f32(d.sc_ln_b, D, "scorer ln bias");
+  sc_w1_ = upload_f32(d.sc_w1, D * D, "scorer w1");
+  sc_b1_ = upload_opt_f32(d.sc_b1, D, "scorer b1");
+  sc_w2_ = upload_f32(d.sc_w2, D, "scorer w2");
+  sc_b2_ = upload_opt_f32(d.sc_b2, 1, "scorer b2");
+  act_w1_ = upload_f32(d.act_w1, 256 * (D + 4), "act w1");
+  act_b1_ = upload_f32(d.act_b1, 256, "act b1");
+  act_w2_ = upload_f32(d.act_w2, static_cast<size_t>(n_act_) * 256, "act w2");
+  act_b2_ = upload_f32(d.act_b2, static_cast<size_t>(n_act_), "act b2");
+}
+
+// ------------------------------------------------------------------ batches --
+BatchPlan Engine::plan(const int64_t* ids, const int64_t* mask, int B, int L,
+                       int32_t* ids_out) const {
+  BatchPlan p;
+  p.B = B;
+  p.L = L;
+  require(L > 0, "sequence length must be positive");
+  if (L > max_len_)
+    fail("sequence length " + std::to_string(L) + " exceeds max_len " + std::to_string(max_len_));
+  p.seq_start.resize(static_cast<size_t>(B));
+  p.q_len.resize(static_cast<size_t>(B));
+  p.k_len.resize(static_cast<size_t>(B));
+  int64_t T = 0;
+  for (int b = 0; b < B; ++b) {
+    int64_t n = 0;
+    for (int i = 0; i < L; ++i) n += mask[static_cast<int64_t>(b) * L + i];
+    if (n < 0 || n > L) fail("attention_mask row " + std::to_string(b) + " is not 0/1");
+    p.k_len[static_cast<size_t>(b)] = static_cast<int32_t>(n);
+    const int rows = pad_rows_ ? L : static_cast<int>(n);
+    p.q_len[static_cast<size_t>(b)] = rows;
+    p.seq_start[static_cast<size_t>(b)] = static_cast<int32_t>(T);
+    T += rows;
+  }
+  if (T > (int64_t{1} << 30)) fail("batch too large");
+  p.T = static_cast<int>(T);
+  p.max_q = 0;
+  for (int b = 0; b < B; ++b) p.max_q = std::max(p.max_q, p.q_len[static_cast<size_t>(b)]);
+  if (ids_out) {
+    for (int b = 0; b < B; ++b) {
+      const int rows = p.q_len[static_cast<size_t>(b)];
+      for (int i = 0; i < rows; ++i) {
+        const int64_t id = ids[static_cast<int64_t>(b) * L + i];
+        if (id < 0 || id >= V_) fail("token id " + std::to_string(id) + " outside the vocabulary");
+        ids_out[p.seq_start[static_cast<size_t>(b)] + i] = static_cast<int32_t>(id);
+      }
+    }
+  }
+  return p;
+}
+
+void Engine::ensure_workspace(int T, int B) {
+  if (T <= cap_T_ && B <= cap_B_) return;
+  hip_check(hipStreamSynchronize(stream_), "sync before workspace growth");
+  const int nT = std::max(T, cap_T_ + cap_T_ / 4);
+  const int nB = std::max(B, cap_B_);
+  const size_t t = static_cast<size_t>(std::max(nT, 1));
+  const size_t D = D_, as = dt_size(act_dt_);
+  ids_.ensure(t * 4);
+  tok_pos_.ensure(t * 4);
+  tok_seq_.ensure(t * 4);
+  seqinfo_.ensure(static_cast<size_t>(4) * std::max(nB, 1) * 4);
+  X_.ensure(t * D * 4);
+  Y_.ensure(t * D * as);
+  QKV_.ensure(t * 3 * D * as);
+  O_.ensure(t * D * as);
+  G_.ensure(t * std::max<size_t>(F_, head_layers_ > 0 ? 4 * D : 0) * as);
+  if (lora_r_ > 0) Z_.ensure(t * static_cast<size_t>(lora_r_) * 4);
+  cap_T_ = nT;
+  cap_B_ = nB;
+  ++ws_gen_;
+  for (auto& kv : graphs_)
+    if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+  graphs_.clear();
+}
+
+void Engine::upload_batch(const BatchPlan& p, const int32_t* h_ids, const int32_t* h_qtype,
+                          hipStream_t st) {
+  // pinned staging: [seq_start | q_len | k_len | qtype] then the token ids
+  const size_t nsi = static_cast<size_t>(4) * p.B;
+  h_stage_.ensure((nsi + (h_ids ? p.T : 0)) * 4);
+  int32_t* s = h_stage_.as<int32_t>();
+  std::memcpy(s, p.seq_start.data(), p.B * 4);
+  std::memcpy(s + p.B, p.q_len.data(), p.B * 4);
+  std::memcpy(s + 2 * p.B, p.k_len.data(), p.B * 4);
+  for (int b = 0; b < p.B; ++b) s[3 * p.B + b] = h_qtype ? h_qtype[b] : 0;
+  hip_check(hipMemcpyAsync(seqinfo_.get(), s, nsi * 4, hipMemcpyHostToDevice, st), "upload seqinfo");
+  if (h_ids) {
+    std::memcpy(s + nsi, h_ids, static_cast<size_t>(p.T) * 4);
+    hip_check(hipMemcpyAsync(ids_.get(), s + nsi, static_cast<size_t>(p.T) * 4,
+                             hipMemcpyHostToDevice, st),
+              "upload ids");
+  }
+}
+
+// ------------------------------------------------------------------ launches --
+void Engine::prof_begin(hipStream_t st) {
+  if (!profile_) return;
+  hipEvent_t e;
+  if (!ev_pool_.empty()) {
+    e = ev_pool_.back();
+    ev_pool_.pop_back();
+  } else {
+    hip_check(hipEventCreate(&e), "hipEventCreate");
+  }
+  hip_check(hipEventRecord(e, st), "hipEventRecord");
+  ev_open_ = e;
+}
+
+void Engine::prof_end(const char* name, hipStream_t st) {
+  if (!profile_) return;
+  hipEvent_t e;
+  if (!ev_pool_.empty()) {
+    e = ev_pool_.back();
+    ev_pool_.pop_back();
+  } else {
+    hip_check(hipEventCreate(&e), "hipEventCreate");
+  }
+  hip_check(hipEventRecord(e, st), "hipEventRecord");
+  prof_pending_.push_back({name, ev_open_, e});
+  ev_open_ = nullptr;
+}
+
+void Engine::prof_collect() {
+  for (auto& p : prof_pending_) {
+    hip_check(hipEventSynchronize(p.b), "hipEventSynchronize");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, p.a, p.b), "hipEventElapsedTime");
+    auto& t = prof_tot_[p.name];
+    std::get<0>(t) = p.name;
+    std::get<1>(t) += ms;
+    std::get<2>(t) += 1;
+    ev_pool_.push_back(p.a);
+    ev_pool_.push_back(p.b);
+  }
+  prof_pending_.clear();
+}
+
+void Engine::set_profile(bool on) {
+  std::lock_guard<std::mutex> lk(mu_);
+  hip_check(hipSetDevice(dev_), "hipSetDevice");
+  if (!on) prof_collect();
+  profile_ = on;
+  if (on) prof_tot_.clear();
+}
+
+std::vector<std::tuple<const char*, double, int64_t>> Engine::profile_totals() {
+  std::lock_guard<std::mutex> lk(mu_);
+  hip_check(hipSetDevice(dev_), "hipSetDevice");
+  prof_collect();
+  std::vector<std::tuple<const char*, double, int64_t>> v;
+  for (auto& kv : prof_tot_) v.push_back(kv.second);
+  return v;
+}
+
+void Engine::gemm(const char* name, const GemmArgs& g, hipStream_t st) {
+  prof_begin(st);
+  launch_gemm(g, st);
+  prof_end(name, st);
+}
+
+void Engine::ln(const char* name, const LnArgs& a, hipStream_t st) {
+  prof_begin(st);
+  launch_ln(a, st);
+  prof_end(name, st);
+}
+
+void Engine::attn(const char* name, const AttnArgs& a, hipStream_t st) {
+  prof_begin(st);
+  launch_attn(a, st);
+  prof_end(name, st);
+}
+
+// ------------------------------------------------------------------ encoder --
+void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X, hipStream_t st) {
+  const int T = p.T, D = D_, F = F_;
+  const int32_t* si = seqinfo_.as<int32_t>();
+  const int32_t* seq_start = si;
+  const int32_t* q_len = si + p.B;
+  const int32_t* k_len = si + 2 * p.B;
+  const int adt = act_dt_;
+  void* Y = Y_.get();
+  void* QKV = QKV_.get();
+  void* O = O_.get();
+  void* G = G_.get();
+
+  launch_token_index(seq_start, q_len, p.B, tok_pos_.as<int>(), tok_seq_.as<int>(), st);
+
+  // src/model.cpp:332-340: X = LN(emb[ids]); layer 0 reads X itself
+  {
+    LnArgs e;
+    e.in = emb_w_.get();
+    e.in_dtype = adt;
+    e.ld_in = D;
+    e.ids = d_ids;
+    e.w = emb_norm_.as<float>();
+    e.eps = eps_;
+    e.x_out = X;
+    e.ld_x = D;
+    if (!layers_[0].has_attn_norm) {
+      e.y_out = Y;
+      e.y_dtype = adt;
+      e.ld_y = D;
+    }
+    e.M = T;
+    e.D = D;
+    ln("emb_ln", e, st);
+  }
+
+  const float scale = 1.0f / std::sqrt(static_cast<float>(Dh_));
+  for (int li = 0; li < nlayers_; ++li) {
+    const LayerDev& ly = layers_[static_cast<size_t>(li)];
+    if (ly.has_attn_norm || li > 0) {
+      LnArgs a;
+      a.in = X;
+      a.in_dtype = DT_F32;
+      a.ld_in = D;
+      a.normalize = ly.has_attn_norm;
+      a.w = ly.has_attn_norm ? ly.attn_norm.as<float>() : nullptr;
+      a.eps = eps_;
+      a.y_out = Y;
+      a.y_dtype = adt;
+      a.ld_y = D;
+      a.M = T;
+      a.D = D;
+      ln("attn_norm", a, st);
+    }
+    {  // qkv = Y . Wqkv^T with RoPE on q, k (src/model.cpp:355-365)
+      GemmArgs g;
+      g.A = Y;
+      g.lda = D;
+      g.W = ly.wqkv.get();
+      g.ldw = D;
+      g.M = T;
+      g.N = 3 * D;
+      g.K = D;
+      g.in_dtype = adt;
+      g.epi = EPI_ROPE;
+      g.out = QKV;
+      g.ldo = 3 * D;
+      g.out_dtype = adt;
+      g.pos = tok_pos_.as<int>();
+      g.rope_cos = (ly.sliding ? rope_cos_slide_ : rope_cos_full_).as<float>();
+      g.rope_sin = (ly.sliding ? rope_sin_slide_ : rope_sin_full_).as<float>();
+      g.rope_dim = D;
+      g.head_dim = Dh_;
+      gemm("gemm_qkv_rope", g, st);
+    }
+    {  // attention (src/model.cpp:381)
+      AttnArgs a;
+      a.q = QKV;
+      a.k = off<char>(QKV, D, adt);
+      a.v = off<char>(QKV, 2 * D, adt);
+      a.ld_q = a.ld_k = a.ld_v = 3 * D;
+      a.o = O;
+      a.ld_o = D;
+      a.dtype = adt;
+      a.seq_start = seq_start;
+      a.q_len = q_len;
+      a.k_len = k_len;
+      a.B = p.B;
+      a.H = H_;
+      a.Dh = Dh_;
+      a.max_q = p.max_q;
+      a.window = ly.window;
+      a.scale = scale;
+      attn("attention", a, st);
+    }
+    {  // X += O . Wo^T (src/model.cpp:389-391)
+      GemmArgs g;
+      g.A = O;
+      g.lda = D;
+      g.W = ly.wo.get();
+      g.ldw = D;
+      g.M = T;
+      g.N = D;
+      g.K = D;
+      g.in_dtype = adt;
+      g.epi = EPI_RESID;
+      g.X = X;
+      g.ldx = D;
+      gemm("gemm_wo_resid", g, st);
+    }
+    {  // Y = mlp_norm(X) (src/model.cpp:392)
+      LnArgs a;
+      a.in = X;
+      a.in_dtype = DT_F32;
+      a.ld_in = D;
+      a.w = ly.mlp_norm.as<float>();
+      a.eps = eps_;
+      a.y_out = Y;
+      a.y_dtype = adt;
+      a.ld_y = D;
+      a.M = T;
+      a.D = D;
+      ln("mlp_norm", a, st);
+    }
+    {  // G = geglu(Y . Wi^T) (src/model.cpp:394)
+      GemmArgs g;
+      g.A = Y;
+      g.lda = D;
+      g.W = ly.wi.get();
+      g.ldw = D;
+      g.M = T;
+      g.N = F;
+      g.K = D;
+      g.in_dtype = adt;
+      g.epi = EPI_GEGLU;
+      g.out = G;
+      g.ldo = F;
+      g.out_dtype = adt;
+      gemm("gemm_wi_geglu", g, st);
+    }
+    {  // X += G . Wo2^T (src/model.cpp:395-397)
+      GemmArgs g;
+      g.A = G;
+      g.lda = F;
+      g.W = ly.wo2.get();
+      g.ldw = F;
+      g.M = T;
+      g.N = D;
+      g.K = F;
+      g.in_dtype = adt;
+      g.epi = EPI_RESID;
+      g.X = X;
+      g.ldx = D;
+      gemm("gemm_wo2_resid", g, st);
+    }
+  }
+  {  // final norm, in place (src/model.cpp:400)
+    LnArgs a;
+    a.in = X;
+    a.in_dtype = DT_F32;
+    a.ld_in = D;
+    a.w = final_norm_.as<float>();
+    a.eps = eps_;
+    a.x_out = X;
+    a.ld_x = D;
+    a.M = T;
+    a.D = D;
+    ln("final_norm", a, st);
+  }
+  if (lora_r_ > 0) {  // h += (h . A^T) . B^T (src/model.cpp:402-407)
+    GemmArgs g;
+    g.A = X;
+    g.lda = D;
+    g.W = lora_a_.get();
+    g.ldw = D;
+    g.M = T;
+    g.N = lora_r_;
+    g.K = D;
+    g.in_dtype = DT_F32;
+    g.epi = EPI_STORE;
+    g.out = Z_.get();
+    g.ldo = lora_r_;
+    g.out_dtype = DT_F32;
+    gemm("gemm_lora_a", g, st);
+    GemmArgs g2;
+    g2.A = Z_.get();
+    g2.lda = lora_r_;
+    g2.W = lora_b_.get();
+    g2.ldw = lora_r_;
+    g2.M = T;
+    g2.N = D;
+    g2.K = lora_r_;
+    g2.in_dtype = DT_F32;
+    g2.epi = EPI_RESID;
+    g2.X = X;
+    g2.ldx = D;
+    gemm("gemm_lora_b", g2, st);
+  }
+}
+
+// src/model.cpp:409-459: type embedding, then N pre-norm TransformerEncoderLayers.
+void Engine::enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st) {
+  const int T = p.T, D = D_;
+  const int32_t* si = seqinfo_.as<int32_t>();
+  const int adt = act_dt_;
+  launch_add_row_embedding(X, D, type_emb_.as<float>(), si + 3 * p.B, tok_seq_.as<int>(), T, D,
+                           st);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(Dh_));
+  for (const HeadDev& hd : head_) {
+    LnArgs a;
+    a.in = X;
+    a.in_dtype = DT_F32;
+    a.ld_in = D;
+    a.w = hd.n1w.as<float>();
+    a.b = hd.n1b.as<float>();
+    a.eps = 1e-5f;
+    a.y_out = Y_.get();
+    a.y_dtype = adt;
+    a.ld_y = D;
+    a.M = T;
+    a.D = D;
+    ln("head_norm1", a, st);
+
+    GemmArgs g;
+    g.A = Y_.get();
+    g.lda = D;
+    g.W = hd.in_w.get();
+    g.ldw = D;
+    g.M = T;
+    g.N = 3 * D;
+    g.K = D;
+    g.in_dtype = adt;
+    g.epi = EPI_STORE;
+    g.out = QKV_.get();
+    g.ldo = 3 * D;
+    g.out_dtype = adt;
+    g.bias = hd.in_b.as<float>();
+    gemm("head_in_proj", g, st);
+
+    AttnArgs at;
+    at.q = QKV_.get();
+    at.k = off<char>(QKV_.get(), D, adt);
+    at.v = off<char>(QKV_.get(), 2 * D, adt);
+    at.ld_q = at.ld_k = at.ld_v = 3 * D;
+    at.o = O_.get();
+    at.ld_o = D;
+    at.dtype = adt;
+    at.seq_start = si;
+    at.q_len = si + p.B;
+    at.k_len = si + 2 * p.B;
+    at.B = p.B;
+    at.H = H_;
+    at.Dh = Dh_;
+    at.max_q = p.max_q;
+    at.window = 0;
+    at.scale = scale;
+    attn("head_attention", at, st);
+
+    GemmArgs go;
+    go.A = O_.get();
+    go.lda = D;
+    go.W = hd.out_w.get();
+    go.ldw = D;
+    go.M = T;
+    go.N = D;
+    go.K = D;
+    go.in_dtype = adt;
+    go.epi = EPI_RESID;
+    go.X = X;
+    go.ldx = D;
+    go.bias = hd.out_b.as<float>();
+    gemm("head_out_proj", go, st);
+
+    LnArgs a2 = a;
+    a2.w = hd.n2w.as<float>();
+    a2.b = hd.n2b.as<float>();
+    ln("head_norm2", a2, st);
+
+    GemmArgs g1;
+    g1.A = Y_.get();
+    g1.lda = D;
+    g1.W = hd.l1w.get();
+    g1.ldw = D;
+    g1.M = T;
+    g1.N = 4 * D;
+    g1.K = D;
+    g1.in_dtype = adt;
+    g1.epi = EPI_STORE;
+    g1.out = G_.get();
+    g1.ldo = 4 * D;
+    g1.out_dtype = adt;
+    g1.bias = hd.l1b.as<float>();
+    g1.act = 2;
+    gemm("head_linear1", g1, st);
+
+    GemmArgs g2;
+    g2.A = G_.get();
+    g2.lda = 4 * D;
+    g2.W = hd.l2w.get();
+    g2.ldw = 4 * D;
+    g2.M = T;
+    g2.N = D;
+    g2.K = 4 * D;
+    g2.in_dtype = adt;
+    g2.epi = EPI_RESID;
+    g2.X = X;
+    g2.ldx = D;
+    g2.bias = hd.l2b.as<float>();
+    gemm("head_linear2", g2, st);
+  }
+}
+
+void Engine::run_device(const BatchPlan& p, const int32_t* d_ids, float* X, bool head,
+                        hipStream_t st) {
+  enqueue_encoder(p, d_ids, X, st);
+  if (head) enqueue_head_layers(p, X, st);
+}
+
+void Engine::run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, float* X,
+                                    bool head, hipStream_t st) {
+  if (!use_graphs_ || profile_) {
+    run_device(p, d_ids, X, head, st);
+    return;
+  }
+  const std::vector<int64_t> key = {p.B,
+                                    p.T,
+                                    p.max_q,
+                                    head ? 1 : 0,
+                                    static_cast<int64_t>(ws_gen_),
+                                    reinterpret_cast<int64_t>(d_ids),
+                                    reinterpret_cast<int64_t>(X),
+                                    reinterpret_cast<int64_t>(st)};
+  auto it = graphs_.find(key);
+  if (it == graphs_.end()) {
+    if (graphs_.size() >= 32) {
+      for (auto& kv : graphs_)
+        if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+      graphs_.clear();
+    }
+    hipGraph_t graph = nullptr;
+    hip_check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
+    try {
+      run_device(p, d_ids, X, head, st);
+    } catch (...) {
+      (void)hipStreamEndCapture(st, &graph);
+      if (graph) (void)hipGraphDestroy(graph);
+      throw;
+    }
+    hip_check(hipStreamEndCapture(st, &graph), "end capture");
+    Graph g;
+    hipError_t e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    hip_check(e, "graph instantiate");
+    it = graphs_.emplace(key, g).first;
+  }
+  hip_check(hipGraphLaunch(it->second.exec, st), "graph launch");
+}
+
+// ------------------------------------------------------------------ entries --
+void Engine::encode(const int64_t* ids, const int64_t* mask, int B, int L, float* hidden) {
+  std::lock_guard<std::mutex> lk(mu_);
+  hip_check(hipSetDevice(dev_), "hipSetDevice");
+  if (B <= 0) return;
+  require(ids && mask && hidden, "encode: null argument");
+  std::vector<int32_t> packed;
+  BatchPlan p0 = plan(ids, mask, B, L, nullptr);
+  packed.resize(static_cast<size_t>(p0.T));
+  BatchPlan p = plan(ids, mask, B, L, packed.data());
+  ensure_workspace(std::max(p.T, 1), B);
+  const size_t D = D_;
+  if (p.T > 0) {
+    upload_batch(p, packed.data(), nullptr, stream_);
+    run_device_maybe_graph(p, ids_.as<int32_t>(), X_.as<float>(), false, stream_);
+  }
+  if (pad_rows_) {
+    if (p.T > 0)
+      hip_check(hipMemcpyAsync(hidden, X_.get(), static_cast<size_t>(p.T) * D * 4,
+                               hipMemcpyDeviceToHost, stream_),
+                "download hidden");
+    hip_check(hipStreamSynchronize(stream_), "encode");
+  } else {
+    h_out_.ensure(std::max<size_t>(static_cast<size_t>(p.T) * D * 4, 4));
+    if (p.T > 0)
+      hip_check(hipMemcpyAsync(h_out_.as<float>(), X_.get(), static_cast<size_t>(p.T) * D * 4,
+                               hipMemcpyDeviceToHost, stream_),
+                "download hidden");
+    hip_check(hipStreamSynchronize(stream_), "encode");
+    std::memset(hidden, 0, static_cast<size_t>(B) * L * D * 4);
+    const float* src = h_out_.as<float>();
+    for (int b = 0; b < B; ++b)
+      std::memcpy(hidden + static_cast<size_t>(b) * L * D,
+                  src + static_cast<size_t>(p.seq_start[static_cast<size_t>(b)]) * D,
+                  static_cast<size_t>(p.q_len[static_cast<size_t>(b)]) * D * 4);
+  }
+  if (profile_) prof_collect();
+}
+
+void Engine::encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, float* d_hidden,
+                           hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(mu_);
+  hip_check(hipSetDevice(dev_), "hipSetDevice");
+  if (B <= 0) return;
+  require(d_ids && h_lens && d_hidden, "encode_device: null argument");
+  hipStream_t st = stream ? stream : stream_;
+  BatchPlan p;
+  p.B = B;
+  p.seq_start.resize(static_cast<size_t>(B));
+  p.q_len.resize(static_cast<size_t>(B));
+  p.k_len.resize(static_cast<size_t>(B));
+  int64_t T = 0;
+  for (int b = 0; b < B; ++b) {
+    const int n = h_lens[b];
+    if (n < 0 || n > max_len_) fail("sequence length outside [0, max_len]");
+    p.seq_start[static_cast<size_t>(b)] = static_cast<int32_t>(T);
+    p.q_len[static_cast<size_t>(b)] = n;
+    p.k_len[static_cast<size_t>(b)] = n;
+    p.max_q = std::max(p.max_q, n);
+    T += n;
+  }
+  if (T > (int64_t{1} << 30)) fail("batch too large");
+  p.T = static_cast<int>(T);
+  p.L = p.max_q;
+  if (p.T == 0) return;
+  ensure_workspace(p.T, B);
+  // The staging buffer is reused by the next call: make sure the previous
+  // upload from it has been consumed before overwriting.
+  hip_check(hipStreamSynchronize(st), "encode_device: previous upload");
+  upload_batch(p, nullptr, nullptr, st);
+  run_device_maybe_graph(p, d_ids, d_hidden, false, st);
+}
+
+void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* marker_pos,
+                     const uint8_t* marker_mask, const int64_t* qtype, int B, int L, int K,
+                     float* logits, float* act) {
+  std::lock_guard<std::mutex> lk(mu_);
+  hip_check(hipSetDevice(dev_), "hipSetDevice");
+  if (B <= 0) return;
+  require(ids && mask && marker_pos && marker_mask && qtype && logits && act,
+          "forward: null argument");
+  require(K > 0, "forward: need at least one marker column");
+  BatchPlan p0 = plan(ids, mask, B, L, nullptr);
+  std::vector<int32_t> packed(static_cast<size_t>(p0.T));
+  BatchPlan p = plan(ids, mask, B, L, packed.data());
+  std::vector<int32_t> qt(static_cast<size_t>(B));
+  for (int b = 0; b < B; ++b) {
+    if (qtype[b] < 0 || qtype[b] > 2) fail("qtype must be 0, 1 or 2");
+    qt[static_cast<size_t>(b)] = static_cast<int32_t>(qtype[b]);
+  }
+  ensure_workspace(std::max(p.T, 1), B);
+  const int D = D_;
+  hipStream_t st = stream_;
+  if (p.T > 0) {
+    upload_batch(p, packed.data(), qt.data(), st);
+    run_device_maybe_graph(p, ids_.as<int32_t>(), X_.as<float>(), true, st);
+  }
+
+  // ---- scorer (src/model.cpp:461-487) on device: gather marker rows and CLS rows
+  const int nmk = B * K, nrow = nmk + B;
+  std::vector<int32_t> idx(static_cast<size_t>(nrow));
+  for (int b = 0; b < B; ++b) {
+    for (int k = 0; k < K; ++k) {
+      int64_t pp = marker_pos[static_cast<int64_t>(b) * K + k];
+      if (pp < 0) pp = 0;
+      if (pp >= L) pp = L - 1;
+      idx[static_cast<size_t>(b) * K + k] =
+          pp < p.q_len[static_cast<size_t>(b)] ? p.seq_start[static_cast<size_t>(b)] +
+                                                     static_cast<int32_t>(pp)
+                                               : -1;
+    }
+    idx[static_cast<size_t>(nmk + b)] =
+        p.q_len[static_cast<size_t>(b)] > 0 ? p.seq_start[static_cast<size_t>(b)] : -1;
+  }
+  tail_idx_.ensure(static_cast<size_t>(nrow) * 4);
+  tail_rows_.ensure(static_cast<size_t>(nrow) * D * 4);
+  tail_s0_.ensure(static_cast<size_t>(nmk) * D * 4);
+  tail_s1_.ensure(static_cast<size_t>(nmk) * D * 4);
+  tail_s2_.ensure(static_cast<size_t>(nmk) * 4);
+  tail_f4_.ensure(static_cast<size_t>(B) * 4 * 4);
+  tail_ain_.ensure(static_cast<size_t>(B) * (D + 4) * 4);
+  tail_ah_.ensure(static_cast<size_t>(B) * 256 * 4);
+  tail_ao_.ensure(static_cast<size_t>(B) * n_act_ * 4);
+  hip_check(hipMemcpyAsync(tail_idx_.get(), idx.data(), idx.size() * 4, hipMemcpyHostToDevice, st),
+            "upload marker rows");
+  launch_gather_rows(X_.as<float>(), D, tail_idx_.as<int32_t>(), nrow, D, tail_rows_.as<float>(),
+                     D, st);
+  {
+    LnArgs a;
+    a.in = tail_rows_.get();
+    a.in_dtype = DT_F32;
+    a.ld_in = D;
+    a.w = sc_ln_w_.as<float>();
+    a.b = sc_ln_b_.as<float>();
+    a.eps = eps_;
+    a.x_out = tail_s0_.as<float>();
+    a.ld_x = D;
+    a.M = nmk;
+    a.D = D;
+    ln("scorer_norm", a, st);
+    GemmArgs g;
+    g.A = tail_s0_.get();
+    g.lda = D;
+    g.W = sc_w1_.get();
+    g.ldw = D;
+    g.M = nmk;
+    g.N = D;
+    g.K = D;
+    g.in_dtype = DT_F32;
+    g.epi = EPI_STORE;
+    g.out = tail_s1_.get();
+    g.ldo = D;
+    g.out_dtype = DT_F32;
+    g.bias = sc_b1_.as<float>();
+    g.act = 1;
+    gemm("scorer_linear1", g, st);
+    GemmArgs g2 = g;
+    g2.A = tail_s1_.get();
+    g2.W = sc_w2_.get();
+    g2.N = 1;
+    g2.out = tail_s2_.get();
+    g2.ldo = 1;
+    g2.bias = sc_b2_.as<float>();
+    g2.act = 0;
+    gemm("scorer_linear2", g2, st);
+  }
+  std::vector<float> s2(static_cast<size_t>(nmk));
+  hip_check(hipMemcpyAsync(s2.data(), tail_s2_.get(), s2.size() * 4, hipMemcpyDeviceToHost, st),
+            "download logits");
+  hip_check(hipStreamSynchronize(st), "forward: scorer");
+  for (int i = 0; i < nmk; ++i) logits[i] = marker_mask[i] ? s2[static_cast<size_t>(i)] : -1e4f;
+
+  // ---- act head (src/model.cpp:489-535): softmax statistics on host, MLP on device
+  std::vector<float> f4(static_cast<size_t>(B) * 4);
+  std::vector<double> pr(static_cast<size_t>(K));
+  for (int b = 0; b < B; ++b) {
+    const float* lg = logits + static_cast<int64_t>(b) * K;
+    float mx = lg[0];
+    for (int j = 1; j < K; ++j) mx = std::max(mx, lg[j]);
+    double s = 0;
+    for (int j = 0; j < K; ++j) {
+      pr[static_cast<size_t>(j)] = std::exp(lg[j] - mx);
+      s += pr[static_cast<size_t>(j)];
+    }
+    for (double& v : pr) v /= s;
+    double top1 = 0, top2 = 0;
+    for (double v : pr) {
+      if (v > top1) {
+        top2 = top1;
+        top1 = v;
+      } else if (v > top2) {
+        top2 = v;
+      }
+    }
+    double ksum = 0;
+    for (int k = 0; k < K; ++k) ksum += marker_mask[static_cast<int64_t>(b) * K + k];
+    const double kf = std::max(2.0, ksum);
+    double ent = 0;
+    for (double v : pr) ent -= v * std::log(std::max(v, 1e-9));
+    ent /= std::log(kf);
+    f4[static_cast<size_t>(b) * 4 + 0] = static_cast<float>(top1);
+    f4[static_cast<size_t>(b) * 4 + 1] = static_cast<float>(top1 - top2);
+    f4[static_cast<size_t>(b) * 4 + 2] = static_cast<float>(ent);
+    f4[static_cast<size_t>(b) * 4 + 3] = static_cast<float>(kf / 255.0);
+  }
+  hip_check(hipMemcpyAsync(tail_f4_.get(), f4.data(), f4.size() * 4, hipMemcpyHostToDevice, st),
+            "upload act features");
+  launch_concat_cols(tail_rows_.as<float>() + static_cast<size_t>(nmk) * D, D, tail_f4_.as<float>(),
+                     4, B, D, tail_ain_.as<float>(), D + 4, st);
+  {
+    GemmArgs g;
+    g.A = tail_ain_.get();
+    g.lda = D + 4;
+    g.W = act_w1_.get();
+    g.ldw = D + 4;
+    g.M = B;
+    g.N = 256;
+    g.K = D + 4;
+    g.in_dtype = DT_F32;
+    g.epi = EPI_STORE;
+    g.out = tail_ah_.get();
+    g.ldo = 256;
+    g.out_dtype = DT_F32;
+    g.bias = act_b1_.as<float>();
+    g.act = 1;
+    gemm("act_linear1", g, st);
+    GemmArgs g2 = g;
+    g2.A = tail_ah_.get();
+    g2.lda = 256;
+    g2.W = act_w2_.get();
+    g2.ldw = 256;
+    g2.N = n_act_;
+    g2.K = 256;
+    g2.out = tail_ao_.get();
+    g2.ldo = n_act_;
+    g2.bias = act_b2_.as<float>();
+    g2.act = 0;
+    gemm("act_linear2", g2, st);
+  }
+  std::vector<float> ao(static_cast<size_t>(B) * n_act_);
+  hip_check(hipMemcpyAsync(ao.data(), tail_ao_.get(), ao.size() * 4, hipMemcpyDeviceToHost, st),
+            "download act");
+  hip_check(hipStreamSynchronize(st), "forward: act head");
+  for (int b = 0; b < B; ++b) {
+    float* a = ao.data() + static_cast<size_t>(b) * n_act_;
+    float amx = a[0];
+    for (int j = 1; j < n_act_; ++j) amx = std::max(amx, a[j]);
+    double as = 0;
+    for (int j = 0; j < n_act_; ++j) {
+      a[j] = std::exp(a[j] - amx);
+      as += a[j];
+    }
+    for (int j = 0; j < n_act_; ++j)
+      act[static_cast<size_t>(b) * n_act_ + j] = static_cast<float>(a[j] / as);
+  }
+  if (profile_) prof_collect();
+}
+
+}  // namespace sjh

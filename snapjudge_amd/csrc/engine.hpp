@@ -1,0 +1,172 @@
+// engine.hpp -- the device-resident DecisionModel (host orchestration).
+//
+// Owns the device copies of all weights, a grow-only workspace, one HIP stream
+// (default priority) and a cache of captured hipGraphs keyed by batch shape.
+// The forward follows src/model.cpp:309-536 op for op; the differences are in
+// layout only:
+//   * tokens are packed: sequence b occupies rows [seq_start[b],
+//     seq_start[b] + n_b) of every [T, .] activation, T = sum of lengths, so
+//     GEMMs and attention touch valid tokens only (pad_rows = 1 keeps the
+//     reference's [B*L] layout and computes padded query rows as it does);
+//   * RoPE is applied in the QKV GEMM epilogue, GEGLU in the Wi GEMM epilogue
+//     and the residual adds in the Wo / Wo2 GEMM epilogues;
+//   * q, k, v stay in the packed (q|k|v)(head)(dim) rows of one [T, 3D]
+//     buffer; attention reads them with strides (no permute copies,
+//     src/model.cpp:368-387).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "snapjudge_hip.h"
+#include "sjh_kernels.hpp"
+
+namespace sjh {
+
+class DevBuf {
+ public:
+  DevBuf() = default;
+  ~DevBuf();
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  DevBuf(DevBuf&& o) noexcept : p_(o.p_), bytes_(o.bytes_) {
+    o.p_ = nullptr;
+    o.bytes_ = 0;
+  }
+  DevBuf& operator=(DevBuf&& o) noexcept;
+  void alloc(size_t bytes);  // frees and reallocates
+  void ensure(size_t bytes); // grows when smaller
+  void* get() const { return p_; }
+  template <typename T>
+  T* as() const { return static_cast<T*>(p_); }
+  size_t bytes() const { return bytes_; }
+
+ private:
+  void* p_ = nullptr;
+  size_t bytes_ = 0;
+};
+
+class PinnedBuf {
+ public:
+  PinnedBuf() = default;
+  ~PinnedBuf();
+  PinnedBuf(const PinnedBuf&) = delete;
+  PinnedBuf& operator=(const PinnedBuf&) = delete;
+  void ensure(size_t bytes);
+  template <typename T>
+  T* as() const { return static_cast<T*>(p_); }
+
+ private:
+  void* p_ = nullptr;
+  size_t bytes_ = 0;
+};
+
+// Device-side batch layout (see the file comment).
+struct BatchPlan {
+  int B = 0, L = 0, T = 0, max_q = 0;
+  std::vector<int32_t> seq_start, q_len, k_len;
+};
+
+class Engine {
+ public:
+  Engine(const sjh_model_desc& d, const sjh_options& o);
+  ~Engine();
+
+  int D() const { return D_; }
+  int H() const { return H_; }
+  int n_act() const { return n_act_; }
+  int precision() const { return prec_; }
+
+  void encode(const int64_t* ids, const int64_t* mask, int B, int L, float* hidden);
+  void forward(const int64_t* ids, const int64_t* mask, const int64_t* marker_pos,
+               const uint8_t* marker_mask, const int64_t* qtype, int B, int L, int K,
+               float* logits, float* act);
+  void encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, float* d_hidden,
+                     hipStream_t stream);
+
+  void set_profile(bool on);
+  std::vector<std::tuple<const char*, double, int64_t>> profile_totals();
+
+ private:
+  struct LayerDev {
+    DevBuf attn_norm, wqkv, wo, mlp_norm, wi, wo2;
+    bool has_attn_norm = false;
+    int window = 0, sliding = 0;
+  };
+  struct HeadDev {
+    DevBuf n1w, n1b, n2w, n2b, in_w, in_b, out_w, out_b, l1w, l1b, l2w, l2b;
+  };
+  struct Graph {
+    hipGraphExec_t exec = nullptr;
+  };
+
+  void stage_weights(const sjh_model_desc& d);
+  BatchPlan plan(const int64_t* ids, const int64_t* mask, int B, int L, int32_t* ids_out) const;
+  void ensure_workspace(int T, int B);
+  void upload_batch(const BatchPlan& p, const int32_t* h_ids, const int32_t* h_qtype,
+                    hipStream_t st);
+  // device work from token ids to the final hidden states in X (and, with
+  // `head`, through the decision-head layers)
+  void run_device(const BatchPlan& p, const int32_t* d_ids, float* X, bool head,
+                  hipStream_t st);
+  void run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, float* X, bool head,
+                              hipStream_t st);
+  void enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X, hipStream_t st);
+  void enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st);
+
+  // launch helpers (record profile events when enabled)
+  void gemm(const char* name, const GemmArgs& g, hipStream_t st);
+  void ln(const char* name, const LnArgs& a, hipStream_t st);
+  void attn(const char* name, const AttnArgs& a, hipStream_t st);
+  void prof_begin(hipStream_t st);
+  void prof_end(const char* name, hipStream_t st);
+  void prof_collect();
+
+  int dev_ = 0;
+  int prec_ = SJH_PREC_BF16;
+  int act_dt_ = DT_BF16;  // activation / GEMM operand type
+  int D_ = 0, H_ = 0, Dh_ = 0, F_ = 0, V_ = 0, nlayers_ = 0, max_pos_ = 0;
+  int n_act_ = 0, head_layers_ = 0, lora_r_ = 0, max_len_ = 0;
+  float eps_ = 1e-5f;
+  bool use_graphs_ = true, pad_rows_ = false;
+
+  DevBuf emb_w_, emb_norm_, final_norm_, type_emb_;
+  DevBuf rope_cos_full_, rope_sin_full_, rope_cos_slide_, rope_sin_slide_;
+  std::vector<LayerDev> layers_;
+  std::vector<HeadDev> head_;
+  DevBuf lora_a_, lora_b_;
+  DevBuf sc_ln_w_, sc_ln_b_, sc_w1_, sc_b1_, sc_w2_, sc_b2_;
+  DevBuf act_w1_, act_b1_, act_w2_, act_b2_;
+
+  // workspace
+  int cap_T_ = 0, cap_B_ = 0;
+  DevBuf ids_, seqinfo_, tok_pos_, tok_seq_;
+  DevBuf X_, Y_, QKV_, O_, G_, Z_;
+  DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_f4_, tail_ain_, tail_ah_,
+      tail_ao_;
+  PinnedBuf h_stage_, h_out_;
+  uint64_t ws_gen_ = 0;
+
+  hipStream_t stream_ = nullptr;
+  std::map<std::vector<int64_t>, Graph> graphs_;
+  std::mutex mu_;
+
+  bool profile_ = false;
+  struct ProfEv {
+    const char* name;
+    hipEvent_t a, b;
+  };
+  std::vector<ProfEv> prof_pending_;
+  std::vector<hipEvent_t> ev_pool_;
+  hipEvent_t ev_open_ = nullptr;
+  std::map<std::string, std::tuple<const char*, double, int64_t>> prof_tot_;
+};
+
+}  // namespace sjh

@@ -1,0 +1,237 @@
+// rows.hip -- row-wise HBM-bound kernels for gfx950: LayerNorm (with the
+// embedding gather and the residual add fused in), RoPE, token indexing,
+// row gathers.
+//
+// One 64-lane wavefront owns one row: the row is read once into registers
+// (coalesced, one float per lane per 64 columns), reduced with cross-lane
+// shuffles, normalised and written once.
+#include "sjh_common.hpp"
+#include "sjh_host.hpp"
+#include "sjh_kernels.hpp"
+
+namespace sjh {
+
+namespace {
+
+constexpr int kLnWaves = 4;        // rows per workgroup
+constexpr int kLnMaxPerLane = 64;  // D <= 4096 (64 lanes x 64 values)
+
+// LayerNorm as src/tensor.cpp:54-79: mean and population variance
+// accumulated in double, inverse std rounded to float, then
+// (x - (float)mean) * inv * w (+ b) in float.
+template <int NPL, typename InT, typename ResT, typename OutT>
+__global__ __launch_bounds__(64 * kLnWaves) void ln_rows_kernel(LnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
+  if (r >= a.M) return;
+  const int D = a.D;
+  const int64_t src_row = a.ids ? static_cast<int64_t>(a.ids[r]) : static_cast<int64_t>(r);
+  const InT* in = static_cast<const InT*>(a.in) + src_row * a.ld_in;
+  const ResT* res = a.resid ? static_cast<const ResT*>(a.resid) + static_cast<int64_t>(r) * a.ld_in
+                            : nullptr;
+  float v[NPL];
+  const int npl = (D + 63) >> 6;
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    if (i < npl) {
+      const int j = i * 64 + lane;
+      float x = 0.f;
+      if (j < D) {
+        x = load_f32(in + j);
+        if (res) x += load_f32(res + j);
+      }
+      v[i] = x;
+      s += static_cast<double>(x);
+    }
+  }
+  if (a.xio) {
+    float* xo = a.xio + static_cast<int64_t>(r) * a.ld_in;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+      if (i < npl && i * 64 + lane < D) xo[i * 64 + lane] = v[i];
+  }
+  float inv = 1.f, fmean = 0.f;
+  if (a.normalize) {
+    const double mean = wave_sum(s) / static_cast<double>(D);
+    double q = 0.0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+      if (i < npl && i * 64 + lane < D) {
+        const double d = static_cast<double>(v[i]) - mean;
+        q += d * d;
+      }
+    const double var = wave_sum(q) / static_cast<double>(D);
+    inv = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
+    fmean = static_cast<float>(mean);
+  }
+  float* xo = a.x_out ? a.x_out + static_cast<int64_t>(r) * a.ld_x : nullptr;
+  OutT* yo = a.y_out ? static_cast<OutT*>(a.y_out) + static_cast<int64_t>(r) * a.ld_y : nullptr;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = i * 64 + lane;
+    if (i < npl && j < D) {
+      float y = v[i];
+      if (a.normalize) {
+        y = (y - fmean) * inv;
+        if (a.w) y = y * a.w[j];
+        if (a.b) y = y + a.b[j];
+      }
+      if (xo) xo[j] = y;
+      if (yo) store_f32(yo + j, y);
+    }
+  }
+}
+
+template <int NPL, typename InT, typename ResT>
+void ln_dispatch_out(const LnArgs& a, hipStream_t st) {
+  dim3 grid((a.M + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
+  if (a.y_dtype == DT_BF16)
+    ln_rows_kernel<NPL, InT, ResT, bf16_t><<<grid, block, 0, st>>>(a);
+  else
+    ln_rows_kernel<NPL, InT, ResT, float><<<grid, block, 0, st>>>(a);
+}
+
+// Per-lane register budget: the smallest of 4 / 16 / 64 values that holds D.
+template <typename InT, typename ResT>
+void ln_dispatch_npl(const LnArgs& a, hipStream_t st) {
+  const int npl = (a.D + 63) / 64;
+  if (npl <= 4)
+    ln_dispatch_out<4, InT, ResT>(a, st);
+  else if (npl <= 16)
+    ln_dispatch_out<16, InT, ResT>(a, st);
+  else
+    ln_dispatch_out<kLnMaxPerLane, InT, ResT>(a, st);
+}
+
+template <typename InT>
+void ln_dispatch_res(const LnArgs& a, hipStream_t st) {
+  if (a.resid_dtype == DT_BF16)
+    ln_dispatch_npl<InT, bf16_t>(a, st);
+  else
+    ln_dispatch_npl<InT, float>(a, st);
+}
+
+// Rotate-half RoPE on packed rows (src/tensor.cpp:257-279); one thread per
+// (row, q/k head, pair).
+template <typename T>
+__global__ void rope_kernel(T* qkv, int64_t M, int64_t ld, const int* pos, int L, int H, int Dh,
+                            const float* cos_t, const float* sin_t) {
+  const int half = Dh / 2;
+  const int64_t per_row = static_cast<int64_t>(2) * H * half;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= M * per_row) return;
+  const int64_t r = idx / per_row;
+  const int rem = static_cast<int>(idx - r * per_row);
+  const int hh = rem / half, d = rem - hh * half;
+  const int p = pos ? pos[r] : static_cast<int>(r % L);
+  T* x = qkv + r * ld + static_cast<int64_t>(hh) * Dh;
+  const float x0 = load_f32(x + d), x1 = load_f32(x + d + half);
+  const float c = cos_t[static_cast<int64_t>(p) * half + d];
+  const float s = sin_t[static_cast<int64_t>(p) * half + d];
+  store_f32(x + d, x0 * c - x1 * s);
+  store_f32(x + d + half, x1 * c + x0 * s);
+}
+
+__global__ void token_index_kernel(const int* seq_start, const int* rows, int* tok_pos,
+                                   int* tok_seq) {
+  const int b = blockIdx.x;
+  const int s0 = seq_start[b], n = rows[b];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    tok_pos[s0 + i] = i;
+    tok_seq[s0 + i] = b;
+  }
+}
+
+__global__ void add_row_embedding_kernel(float* X, int64_t ldx, const float* table,
+                                         const int* sel, const int* tok_seq, int T, int D) {
+  const int t = blockIdx.x;
+  if (t >= T) return;
+  const float* te = table + static_cast<int64_t>(sel[tok_seq[t]]) * D;
+  float* x = X + static_cast<int64_t>(t) * ldx;
+  for (int j = threadIdx.x; j < D; j += blockDim.x) x[j] += te[j];
+}
+
+__global__ void gather_rows_kernel(const float* src, int64_t ld_src, const int* idx, int n, int D,
+                                   float* dst, int64_t ld_dst) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  const int s = idx[i];
+  float* d = dst + static_cast<int64_t>(i) * ld_dst;
+  for (int j = threadIdx.x; j < D; j += blockDim.x)
+    d[j] = s >= 0 ? src[static_cast<int64_t>(s) * ld_src + j] : 0.f;
+}
+
+__global__ void concat_cols_kernel(const float* src, int64_t ld_src, const float* extra, int E,
+                                   int n, int D, float* dst, int64_t ld_dst) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  float* d = dst + static_cast<int64_t>(i) * ld_dst;
+  for (int j = threadIdx.x; j < D + E; j += blockDim.x)
+    d[j] = j < D ? src[static_cast<int64_t>(i) * ld_src + j] : extra[static_cast<int64_t>(i) * E + (j - D)];
+}
+
+}  // namespace
+
+void launch_ln(const LnArgs& a, hipStream_t st) {
+  if (a.M <= 0) return;
+  require(a.D > 0 && a.D <= 64 * kLnMaxPerLane, "layer_norm: D must be in [1, 4096]");
+  require(a.in != nullptr, "layer_norm: null input");
+  require(a.ld_in >= a.D, "layer_norm: ld_in < D");
+  require(!a.xio || (a.in_dtype == DT_F32 && a.ids == nullptr),
+        "layer_norm: residual write-back needs fp32 rows without a gather");
+  require(!a.x_out || a.ld_x >= a.D, "layer_norm: ld_x < D");
+  require(!a.y_out || a.ld_y >= a.D, "layer_norm: ld_y < D");
+  if (a.in_dtype == DT_BF16)
+    ln_dispatch_res<bf16_t>(a, st);
+  else
+    ln_dispatch_res<float>(a, st);
+  check_launch("layer_norm");
+}
+
+void launch_rope(void* qkv, int dtype, int64_t M, int64_t ld, const int* pos, int L, int H,
+                 int Dh, const float* cos_t, const float* sin_t, hipStream_t st) {
+  if (M <= 0) return;
+  require(Dh > 0 && Dh % 2 == 0, "rope: head_dim must be even");
+  require(ld >= static_cast<int64_t>(3) * H * Dh, "rope: row stride < 3*H*Dh");
+  require(pos != nullptr || L > 0, "rope: need positions or L > 0");
+  const int64_t total = M * 2 * H * (Dh / 2);
+  dim3 block(256), grid(static_cast<unsigned>((total + 255) / 256));
+  if (dtype == DT_BF16)
+    rope_kernel<bf16_t><<<grid, block, 0, st>>>(static_cast<bf16_t*>(qkv), M, ld, pos, L, H, Dh,
+                                                 cos_t, sin_t);
+  else
+    rope_kernel<float><<<grid, block, 0, st>>>(static_cast<float*>(qkv), M, ld, pos, L, H, Dh,
+                                               cos_t, sin_t);
+  check_launch("rope");
+}
+
+void launch_token_index(const int* seq_start, const int* rows, int B, int* tok_pos, int* tok_seq,
+                        hipStream_t st) {
+  if (B <= 0) return;
+  token_index_kernel<<<B, 256, 0, st>>>(seq_start, rows, tok_pos, tok_seq);
+  check_launch("token_index");
+}
+
+void launch_add_row_embedding(float* X, int64_t ldx, const float* table, const int* sel,
+                              const int* tok_seq, int T, int D, hipStream_t st) {
+  if (T <= 0) return;
+  add_row_embedding_kernel<<<T, 256, 0, st>>>(X, ldx, table, sel, tok_seq, T, D);
+  check_launch("add_row_embedding");
+}
+
+void launch_gather_rows(const float* src, int64_t ld_src, const int* idx, int n, int D,
+                        float* dst, int64_t ld_dst, hipStream_t st) {
+  if (n <= 0) return;
+  gather_rows_kernel<<<n, 256, 0, st>>>(src, ld_src, idx, n, D, dst, ld_dst);
+  check_launch("gather_rows");
+}
+
+void launch_concat_cols(const float* src, int64_t ld_src, const float* extra, int E, int n, int D,
+                        float* dst, int64_t ld_dst, hipStream_t st) {
+  if (n <= 0) return;
+  concat_cols_kernel<<<n, 256, 0, st>>>(src, ld_src, extra, E, n, D, dst, ld_dst);
+  check_launch("concat_cols");
+}
+
+}  // namespace sjh

@@ -1,0 +1,28 @@
+// sjh_host.hpp -- host-side error helpers shared by the launchers and engine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stdexcept>
+#include <string>
+
+namespace sjh {
+
+[[noreturn]] inline void fail(const std::string& what) {
+  throw std::runtime_error("snapjudge HIP: " + what);
+}
+
+inline void require(bool ok, const char* what) {
+  if (!ok) fail(what);
+}
+
+inline void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+inline void check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) fail(std::string("launch ") + what + ": " + hipGetErrorString(e));
+}
+
+}  // namespace sjh

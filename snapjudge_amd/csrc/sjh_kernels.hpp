@@ -1,0 +1,122 @@
+// sjh_kernels.hpp -- host-side launch interface of the gfx950 kernels.
+//
+// Every launcher validates the shapes its kernel assumes and throws
+// std::runtime_error naming the violated condition before anything reaches the
+// GPU, so a bad call never becomes an out-of-bounds access.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sjh {
+
+enum DType : int { DT_F32 = 0, DT_BF16 = 1 };
+
+// GEMM epilogues, applied to an fp32 tile staged in LDS.
+enum Epi : int {
+  EPI_STORE = 0,  // out = act(acc + bias)                (bias optional)
+  EPI_RESID = 1,  // X (fp32) += acc + bias                (bias optional)
+  EPI_ROPE = 2,   // packed (q|k|v) output, rotate-half RoPE on q and k
+  EPI_GEGLU = 3,  // out[:, j] = gelu(acc_in[:, j]) * acc_gate[:, j]
+};
+
+// out[M, N] = epi(A[M, K] . W[N_w, K]^T).  For EPI_GEGLU, N = F and W is the
+// reference's [2F, K] Wi (rows [0, F) input half, [F, 2F) gate half).
+struct GemmArgs {
+  const void* A = nullptr;
+  int64_t lda = 0;
+  const void* W = nullptr;
+  int64_t ldw = 0;
+  int M = 0, N = 0, K = 0;
+  int in_dtype = DT_BF16;  // A and W
+  int epi = EPI_STORE;
+  void* out = nullptr;  // STORE / ROPE / GEGLU
+  int64_t ldo = 0;
+  int out_dtype = DT_BF16;
+  const float* bias = nullptr;  // [N]
+  int act = 0;                  // 0 none, 1 erf-GELU, 2 ReLU (STORE)
+  float* X = nullptr;           // RESID
+  int64_t ldx = 0;
+  const int* pos = nullptr;  // ROPE: position of each row
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;  // [max_pos, head_dim/2]
+  int rope_dim = 0;                 // D: columns [0, 2D) are q and k
+  int head_dim = 0;
+};
+void launch_gemm(const GemmArgs& g, hipStream_t st);
+
+// Row LayerNorm over [M, D] rows (src/tensor.cpp:54-79 semantics).
+//   input row r = in[(ids ? ids[r] : r) * ld_in]
+//   if resid: x = in_row + resid_row, written back to xio (fp32)
+//   y = normalize ? LN(x) * w (+ b) : x
+//   x_out (fp32, optional) and y_out (y_dtype, optional) receive y.
+struct LnArgs {
+  const void* in = nullptr;
+  int in_dtype = DT_F32;
+  int64_t ld_in = 0;
+  const int* ids = nullptr;
+  const void* resid = nullptr;  // optional residual added first (resid_dtype)
+  int resid_dtype = DT_BF16;
+  float* xio = nullptr;  // where x = in + resid is written back (fp32 rows, ld_in)
+  bool normalize = true;
+  const float* w = nullptr;
+  const float* b = nullptr;
+  float eps = 1e-5f;
+  float* x_out = nullptr;
+  int64_t ld_x = 0;
+  void* y_out = nullptr;
+  int y_dtype = DT_BF16;
+  int64_t ld_y = 0;
+  int M = 0, D = 0;
+};
+void launch_ln(const LnArgs& a, hipStream_t st);
+
+// Non-causal attention over a varlen batch.  Sequence b owns rows
+// [seq_start[b], seq_start[b] + max(q_len[b], k_len[b])); its queries are the
+// first q_len[b] rows and its keys/values the first k_len[b] rows.  Head h of
+// row t sits at q + t*ld_q + h*Dh (same for k, v, o).  window > 0 restricts
+// query i to keys |i - j| <= window (src/tensor.cpp:186-192).  A null
+// seq_start means seq_start[b] = b * uniform_L; a null q_len means
+// q_len[b] = uniform_L (the reference's padded [B, L] layout).
+struct AttnArgs {
+  const void* q = nullptr;
+  const void* k = nullptr;
+  const void* v = nullptr;
+  int64_t ld_q = 0, ld_k = 0, ld_v = 0;
+  void* o = nullptr;
+  int64_t ld_o = 0;
+  int dtype = DT_BF16;
+  const int* seq_start = nullptr;
+  const int* q_len = nullptr;
+  const int* k_len = nullptr;
+  int B = 0, H = 0, Dh = 0;
+  int max_q = 0;  // upper bound of q_len over the batch (grid size)
+  int uniform_L = 0;
+  int window = 0;
+  float scale = 0.f;  // 1/sqrt(Dh)
+};
+void launch_attn(const AttnArgs& a, hipStream_t st);
+
+// Standalone RoPE on packed (q|k|v)(head)(dim) rows, position = pos[r]
+// (or r % L when pos is null), as src/tensor.cpp:257-279.
+void launch_rope(void* qkv, int dtype, int64_t M, int64_t ld, const int* pos, int L, int H,
+                 int Dh, const float* cos_t, const float* sin_t, hipStream_t st);
+
+// Fill tok_pos[t] (position inside its sequence) and tok_seq[t] for the rows
+// [seq_start[b], seq_start[b] + rows[b]) of every sequence.
+void launch_token_index(const int* seq_start, const int* rows, int B, int* tok_pos,
+                        int* tok_seq, hipStream_t st);
+
+// X[t, :] += table[sel[tok_seq[t]], :] for t < T (type embedding of a row's qtype).
+void launch_add_row_embedding(float* X, int64_t ldx, const float* table, const int* sel,
+                              const int* tok_seq, int T, int D, hipStream_t st);
+
+// dst[i, :] = idx[i] >= 0 ? src[idx[i], :] : 0   (fp32 rows)
+void launch_gather_rows(const float* src, int64_t ld_src, const int* idx, int n, int D,
+                        float* dst, int64_t ld_dst, hipStream_t st);
+
+// dst[i, :D] = src[i, :D]; dst[i, D:D+E] = extra[i, :E]   (fp32)
+void launch_concat_cols(const float* src, int64_t ld_src, const float* extra, int E, int n,
+                        int D, float* dst, int64_t ld_dst, hipStream_t st);
+
+}  // namespace sjh

@@ -1,0 +1,217 @@
+"""GPU parity of every kernel-level C ABI entry point against the oracle.
+
+Inputs are bf16-representable so the bf16 kernels and the fp32 oracle see the
+same values; tolerances: fp32 paths 1e-5 relative (summation order), bf16
+outputs one bf16 rounding (2^-8 relative) plus accumulation-order noise.
+Device memory and the stream come from torch (plumbing only); every compute
+call goes through libsnapjudge_hip.so."""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+import snapjudge_amd as sj
+from snapjudge_amd.synth import bf16_round
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+BF, F32 = sj.SJH_BF16, sj.SJH_F32
+
+
+def dev(a: np.ndarray, dtype):
+    t = torch.from_numpy(np.ascontiguousarray(a, np.float32))
+    return t.to(dtype=dtype).cuda()
+
+
+def host(t) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+def stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def P(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def call(fn, *args):
+    rc = fn(*args)
+    if rc != 0:
+        raise sj.SjhError(rc, sj.lib().sjh_last_error().decode())
+    torch.cuda.synchronize()
+
+
+def rel_err(got, want):
+    return float(np.abs(got - want).max() / (np.abs(want).max() + 1e-30))
+
+
+def rnd(rng, shape, scale=1.0):
+    return bf16_round((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 256, 128), (1, 128, 64), (130, 384, 192), (1000, 2304, 768)])
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_gemm_bf16_mfma(orc, M, N, K, act):
+    print(f"gemm bf16 M={M} N={N} K={K} act={act}", flush=True)
+    rng = np.random.default_rng(M + N + K + act)
+    a, w, b = rnd(rng, (M, K)), rnd(rng, (N, K), 0.1), rnd(rng, N)
+    A, W, Bv = dev(a, torch.bfloat16), dev(w, torch.bfloat16), dev(b, torch.float32)
+    Cout = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    call(sj.lib().sjh_gemm, P(A), P(W), P(Bv), P(Cout), M, N, K, act, BF, stream())
+    want = orc.gemm_nt(a, w, b, act)
+    assert rel_err(host(Cout), want) < 8e-3
+
+
+def test_gemm_bf16_identity_layout():
+    # W = [I | 0]: C must reproduce A's first N columns exactly (catches any
+    # lane/row permutation in the MFMA operand or accumulator layout)
+    rng = np.random.default_rng(0)
+    M, N, K = 256, 128, 192
+    a = rnd(rng, (M, K))
+    w = np.zeros((N, K), np.float32)
+    w[np.arange(N), np.arange(N)] = 1.0
+    A, W = dev(a, torch.bfloat16), dev(w, torch.bfloat16)
+    Cout = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    call(sj.lib().sjh_gemm, P(A), P(W), None, P(Cout), M, N, K, 0, BF, stream())
+    assert np.array_equal(host(Cout), a[:, :N])
+
+
+@pytest.mark.parametrize("M,N,K", [(37, 50, 19), (64, 64, 64), (5, 1, 772), (200, 96, 33)])
+def test_gemm_fp32_generic(orc, M, N, K):
+    rng = np.random.default_rng(M * N + K)
+    a, w = rng.standard_normal((M, K)).astype(np.float32), rng.standard_normal((N, K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    for act in (0, 1, 2):
+        A, W, Bv = dev(a, torch.float32), dev(w, torch.float32), dev(b, torch.float32)
+        Cout = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        call(sj.lib().sjh_gemm, P(A), P(W), P(Bv), P(Cout), M, N, K, act, F32, stream())
+        assert rel_err(host(Cout), orc.gemm_nt(a, w, b, act)) < 1e-5
+
+
+@pytest.mark.parametrize("dtype,M,F,K", [("bf16", 200, 128, 128), ("bf16", 77, 1152, 768),
+                                         ("f32", 33, 9, 13), ("bf16", 20, 40, 24)])
+def test_gemm_geglu(orc, dtype, M, F, K):
+    print(f"geglu {dtype} M={M} F={F} K={K}", flush=True)
+    rng = np.random.default_rng(F)
+    a, wi = rnd(rng, (M, K)), rnd(rng, (2 * F, K), 0.2)
+    tdt, cdt = (torch.bfloat16, BF) if dtype == "bf16" else (torch.float32, F32)
+    A, W = dev(a, tdt), dev(wi, tdt)
+    Cout = torch.empty((M, F), dtype=tdt, device="cuda")
+    call(sj.lib().sjh_gemm_geglu, P(A), P(W), P(Cout), M, F, K, cdt, stream())
+    tol = 8e-3 if dtype == "bf16" else 1e-5
+    assert rel_err(host(Cout), orc.gemm_geglu(a, wi)) < tol
+
+
+@pytest.mark.parametrize("dtype,M,D,K", [("bf16", 300, 768, 1152), ("f32", 45, 24, 40)])
+def test_gemm_residual(orc, dtype, M, D, K):
+    rng = np.random.default_rng(K)
+    a, w = rnd(rng, (M, K)), rnd(rng, (D, K), 0.05)
+    x0 = rng.standard_normal((M, D)).astype(np.float32)
+    tdt, cdt = (torch.bfloat16, BF) if dtype == "bf16" else (torch.float32, F32)
+    A, W, X = dev(a, tdt), dev(w, tdt), dev(x0, torch.float32)
+    call(sj.lib().sjh_gemm_residual, P(A), P(W), P(X), M, D, K, cdt, stream())
+    want = x0 + orc.gemm_nt(a, w)
+    assert float(np.abs(host(X) - want).max()) < (2e-4 if dtype == "bf16" else 1e-5)
+
+
+@pytest.mark.parametrize("D", [16, 768, 1024, 1030])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_add_ln(orc, D, dtype):
+    rng = np.random.default_rng(D)
+    M = 37
+    x = (rng.standard_normal((M, D)) * 2 + 0.5).astype(np.float32)
+    r = rnd(rng, (M, D))
+    w, b = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    tdt, cdt = (torch.bfloat16, BF) if dtype == "bf16" else (torch.float32, F32)
+    for residual in (0, 1):
+        for bias in (0, 1):
+            X, R = dev(x, torch.float32), dev(r, tdt)
+            Wt, Bt = dev(w, torch.float32), dev(b, torch.float32)
+            Y = torch.empty((M, D), dtype=tdt, device="cuda")
+            call(sj.lib().sjh_add_ln, P(X), P(R), P(Wt), P(Bt), P(Y), M, D, C.c_float(1e-5),
+                 residual, bias, cdt, stream())
+            xs = x + r if residual else x
+            want = orc.layer_norm(xs, w, b if bias else None, 1e-5)
+            assert float(np.abs(host(X) - xs).max()) <= 1e-6
+            tol = 1e-5 if dtype == "f32" else 1e-2 * float(np.abs(want).max())
+            assert float(np.abs(host(Y) - want).max()) <= tol
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_rope(orc, dtype):
+    rng = np.random.default_rng(3)
+    M, L, H, Dh = 40, 13, 3, 64
+    qkv = rnd(rng, (M, 3 * H * Dh))
+    c, s = orc.rope_table(160000.0, L, Dh)
+    tdt, cdt = (torch.bfloat16, BF) if dtype == "bf16" else (torch.float32, F32)
+    Q, Ct, St = dev(qkv, tdt), dev(c, torch.float32), dev(s, torch.float32)
+    call(sj.lib().sjh_rope, P(Q), P(Ct), P(St), M, L, H, Dh, cdt, stream())
+    want = orc.rope_inplace(qkv, c, s, L, H, Dh)
+    tol = 2e-6 if dtype == "f32" else 1e-2
+    assert float(np.abs(host(Q) - want).max()) <= tol * max(1.0, float(np.abs(want).max()))
+
+
+def _attn_case(orc, dtype, B, L, H, Dh, lens, window, seed):
+    rng = np.random.default_rng(seed)
+    qkv = rnd(rng, (B, L, 3, H, Dh))
+    tdt, cdt = (torch.bfloat16, BF) if dtype == "bf16" else (torch.float32, F32)
+    Q = dev(qkv.reshape(B * L, 3 * H * Dh), tdt)
+    Lens = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    O = torch.full((B * L, H * Dh), 7.0, dtype=tdt, device="cuda")
+    call(sj.lib().sjh_attn, P(Q), P(Lens), P(O), B, L, H, Dh, window, cdt, stream())
+    q, k, v = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
+    want = orc.attention(q, k, v, np.array(lens, np.int64), window)  # [B, H, L, Dh]
+    want = want.transpose(0, 2, 1, 3).reshape(B * L, H * Dh)
+    return host(O), want
+
+
+@pytest.mark.parametrize("dtype,Dh", [("f32", 16), ("f32", 64), ("bf16", 64), ("bf16", 32)])
+@pytest.mark.parametrize("window", [0, 2, 40])
+def test_attention_reference_layout(orc, dtype, Dh, window):
+    print(f"attn {dtype} Dh={Dh} window={window}", flush=True)
+    B, L, H = 4, 150, 2
+    lens = [150, 71, 1, 0]
+    got, want = _attn_case(orc, dtype, B, L, H, Dh, lens, window, seed=Dh + window)
+    tol = 2e-5 if dtype == "f32" else 2e-2
+    assert float(np.abs(got - want).max()) <= tol
+
+
+def test_attention_long_context_sampled_rows():
+    # S = 8192: check sampled query rows against a float64 reference of just those rows
+    B, L, H, Dh = 2, 8192, 2, 64
+    lens = [8192, 5000]
+    rng = np.random.default_rng(8)
+    qkv = rnd(rng, (B, L, 3, H, Dh))
+    Q = dev(qkv.reshape(B * L, 3 * H * Dh), torch.bfloat16)
+    Lens = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    O = torch.empty((B * L, H * Dh), dtype=torch.bfloat16, device="cuda")
+    call(sj.lib().sjh_attn, P(Q), P(Lens), P(O), B, L, H, Dh, 0, BF, stream())
+    got = host(O).reshape(B, L, H, Dh)
+    for b in range(B):
+        for i in (0, 1, 4095, 4999, 5000, 8191):
+            for h in range(H):
+                q = qkv[b, i, 0, h].astype(np.float64)
+                k = qkv[b, :lens[b], 1, h].astype(np.float64)
+                v = qkv[b, :lens[b], 2, h].astype(np.float64)
+                s = k @ q / math.sqrt(Dh)
+                p = np.exp(s - s.max())
+                want = (p / p.sum()) @ v
+                assert float(np.abs(got[b, i, h] - want).max()) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_embed_ln(orc, dtype):
+    rng = np.random.default_rng(12)
+    V, D, M = 300, 768, 50
+    table = rnd(rng, (V, D), 0.02)
+    ids = rng.integers(0, V, size=M).astype(np.int32)
+    w = rng.standard_normal(D).astype(np.float32)
+    tdt, cdt = (torch.bfloat16, BF) if dtype == "bf16" else (torch.float32, F32)
+    T, I, Wt = dev(table, tdt), torch.from_numpy(ids).cuda(), dev(w, torch.float32)
+    X = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    call(sj.lib().sjh_embed_ln, P(T), P(I), P(Wt), P(X), M, D, C.c_float(1e-5), cdt, stream())
+    want = orc.layer_norm(table[ids], w, None, 1e-5)
+    assert float(np.abs(host(X) - want).max()) <= 1e-5 * max(1.0, float(np.abs(want).max()))
