@@ -11,7 +11,7 @@
 // as the B operand of the second MFMA once the key order inside a 16-key
 // step is taken as the MFMA's k order, so P never leaves registers.
 //
-// Generic path (fp32 or bf16, head_dim 16/32/64/128): one thread per query,
+// Generic path (fp32 or bf16, head_dim 8/16/32/64/128): one thread per query,
 // K/V tiles of 32 keys in LDS (broadcast reads), blocked online softmax with
 // expf.  It serves the fp32 parity mode.
 //
@@ -42,7 +42,9 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
   const int qlen = a.q_len ? a.q_len[b] : a.uniform_L;
   const int q0 = blockIdx.x * kQ;
   if (q0 >= qlen) return;
-  const int klen = a.k_len[b];
+  // keys never extend past the rows a sequence owns (a caller's k_len > L in
+  // the padded layout is clamped rather than read out of bounds)
+  const int klen = a.seq_start ? a.k_len[b] : max(0, min(a.k_len[b], a.uniform_L));
   const int64_t row0 = a.seq_start ? a.seq_start[b] : static_cast<int64_t>(b) * a.uniform_L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hb = lane >> 5;
@@ -200,7 +202,9 @@ __global__ __launch_bounds__(gQ) void attn_generic_kernel(AttnArgs a) {
   const int qlen = a.q_len ? a.q_len[b] : a.uniform_L;
   const int q0 = blockIdx.x * gQ;
   if (q0 >= qlen) return;
-  const int klen = a.k_len[b];
+  // keys never extend past the rows a sequence owns (a caller's k_len > L in
+  // the padded layout is clamped rather than read out of bounds)
+  const int klen = a.seq_start ? a.k_len[b] : max(0, min(a.k_len[b], a.uniform_L));
   const int64_t row0 = a.seq_start ? a.seq_start[b] : static_cast<int64_t>(b) * a.uniform_L;
   const int tid = threadIdx.x;
   const int qi = q0 + tid;
@@ -277,11 +281,12 @@ template <typename T>
 void launch_generic(const AttnArgs& a, hipStream_t st) {
   dim3 grid((a.max_q + gQ - 1) / gQ, a.H, a.B), block(gQ);
   switch (a.Dh) {
+    case 8: attn_generic_kernel<T, 8><<<grid, block, 0, st>>>(a); break;
     case 16: attn_generic_kernel<T, 16><<<grid, block, 0, st>>>(a); break;
     case 32: attn_generic_kernel<T, 32><<<grid, block, 0, st>>>(a); break;
     case 64: attn_generic_kernel<T, 64><<<grid, block, 0, st>>>(a); break;
     case 128: attn_generic_kernel<T, 128><<<grid, block, 0, st>>>(a); break;
-    default: fail("attention: head_dim must be 16, 32, 64 or 128");
+    default: fail("attention: head_dim must be 8, 16, 32, 64 or 128");
   }
 }
 

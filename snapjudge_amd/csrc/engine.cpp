@@ -164,6 +164,7 @@ Engine::~Engine() {
     (void)hipEventDestroy(p.b);
   }
   for (hipEvent_t e : ev_pool_) (void)hipEventDestroy(e);
+  if (ev_null_) (void)hipEventDestroy(ev_null_);
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -810,6 +811,8 @@ void Engine::encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, f
   hip_check(hipSetDevice(dev_), "hipSetDevice");
   if (B <= 0) return;
   require(d_ids && h_lens && d_hidden, "encode_device: null argument");
+  // NULL selects the model's own stream, ordered after and before the legacy
+  // null stream so that NULL behaves like the default stream for the caller.
   hipStream_t st = stream ? stream : stream_;
   BatchPlan p;
   p.B = B;
@@ -834,8 +837,17 @@ void Engine::encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, f
   // The staging buffer is reused by the next call: make sure the previous
   // upload from it has been consumed before overwriting.
   hip_check(hipStreamSynchronize(st), "encode_device: previous upload");
+  if (!stream) {
+    if (!ev_null_) hip_check(hipEventCreateWithFlags(&ev_null_, hipEventDisableTiming), "event");
+    hip_check(hipEventRecord(ev_null_, nullptr), "record null stream");
+    hip_check(hipStreamWaitEvent(st, ev_null_, 0), "wait null stream");
+  }
   upload_batch(p, nullptr, nullptr, st);
   run_device_maybe_graph(p, d_ids, d_hidden, false, st);
+  if (!stream) {
+    hip_check(hipEventRecord(ev_null_, st), "record model stream");
+    hip_check(hipStreamWaitEvent(nullptr, ev_null_, 0), "null stream waits");
+  }
 }
 
 void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* marker_pos,

@@ -155,6 +155,7 @@ class Engine {
   uint64_t ws_gen_ = 0;
 
   hipStream_t stream_ = nullptr;
+  hipEvent_t ev_null_ = nullptr;  // orders NULL-stream callers of encode_device
   std::map<std::vector<int64_t>, Graph> graphs_;
   std::mutex mu_;
 
