@@ -8,15 +8,15 @@ random N(0, 0.02) bf16 weights (seed 0), batch 64 x seq 512, row lengths
 ids already resident in HBM (sjh_model_encode_device).
 
 value = valid (non-pad) encoder tokens per second.  Also reported:
-  roofline      -- the dominant kernel (the bf16 MFMA projection GEMM that
+  roofline      -- the dominant kernel (gemm_bf16_dma_kernel, the bf16 MFMA GEMM that
                    serves QKV+RoPE, Wo+residual, Wi+GEGLU, Wo2+residual):
                    algorithmic FLOPs per launch / mean launch time, measured
-                   with hipEvents on the model's stream over a profiled
-                   repeat of the timed steps;
+                   with a hipEvent pair around every launch on the model's
+                   stream during the timed steps;
   attention_mfma_frac -- the attention kernel's algorithmic FLOPs
                    (4*D*sum(n^2) per layer) over its time, vs bf16 peak;
   p50_latency_b1_ms -- config 2 (batch 1, seq 128, no padding) encoder
-                   latency, hipGraph replay, p50 of 50;
+                   latency, hipGraph replay, p50 of 50 (--no-latency skips it);
   cpu_baseline  -- the reference's own CPU forward (oracle/_ref, compiled
                    from its sources, no-BLAS build) on a bounded sample of the
                    same workload, extrapolated by layers.
@@ -75,17 +75,34 @@ def cpu_baseline(w, rl, enc, ids, mask, lens, layers_full):
                       f"{layers_full} layers: {secs:.1f} s, extrapolated x{layers_full}"}
 
 
+def copy_probe(mib):
+    """Plain device-to-device copy of a known size (torch's copy kernel): the
+    calibration run for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_each_way": n * 4, "launches": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-latency", action="store_true",
+                    help="skip the config-2 (batch 1) latency leg")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="also run a plain copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; the encoder shards across GPUs by "
-              "sequence with no exchange (see DESIGN.md) but no multi-GPU path is built.",
-              file=sys.stderr)
+              "sequence with no exchange, but no multi-GPU path is built.", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -97,11 +114,15 @@ def main():
     p = synth.PRESETS["cfg3"]
     rl, enc, w = synth.make_model(**p, seed=0)
     cfg = synth.flat_cfg(rl, enc)
-    D, F, NL, H = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"], cfg["num_attention_heads"]
+    D, F, NL = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
     ids, mask, lens = synth.make_batch(B, S, LO, HI, cfg["vocab_size"], seed=1)
     T = int(lens.sum())
 
-    model = sj.Model(w, cfg, precision=sj.SJH_PREC_BF16, use_graphs=True)
+    # At this size every launch runs for tens of microseconds, so the work is
+    # enqueued launch by launch (no graph) with a hipEvent pair around each
+    # launch on the model's stream: the timed steps themselves give the
+    # per-kernel durations the roofline uses.
+    model = sj.Model(w, cfg, precision=sj.SJH_PREC_BF16, use_graphs=False)
     packed = np.concatenate([ids[b, :lens[b]] for b in range(B)]).astype(np.int32)
     d_ids = torch.from_numpy(packed).cuda()
     d_out = torch.empty((T, D), dtype=torch.float32, device="cuda")
@@ -114,21 +135,18 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    model.profile(True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    prof = model.profile_read()
+    model.profile(False)
     ms_per_step = elapsed * 1e3 / args.steps
     value = T * args.steps / elapsed
 
-    # profiled repeat of the timed steps: hipEvents around every launch
-    model.profile(True)
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    prof = model.profile_read()
-    model.profile(False)
     gemm_ms = sum(prof[n][0] for n in GEMM_NAMES if n in prof)
     gemm_launches = sum(prof[n][1] for n in GEMM_NAMES if n in prof)
     gemm_flops_step = gemm_flops_per_token(D, F, NL) * T
@@ -138,23 +156,28 @@ def main():
     attn_ms, attn_n = prof.get("attention", (0.0, 0))
     attn_flops_step = NL * 4.0 * D * float((lens.astype(np.float64) ** 2).sum())
     attn_tflops = attn_flops_step * args.steps / (attn_ms / 1e3) / 1e12 if attn_ms else 0.0
-
-    # config 2: batch 1, seq 128, p50 latency (graph replay)
-    rng = np.random.default_rng(7)
-    ids2 = rng.integers(0, cfg["vocab_size"], size=128).astype(np.int32)
-    d_ids2 = torch.from_numpy(ids2).cuda()
-    d_out2 = torch.empty((128, D), dtype=torch.float32, device="cuda")
-    l2 = np.array([128], np.int32)
-    lat = []
-    for i in range(60):
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        model.encode_device(d_ids2.data_ptr(), l2, d_out2.data_ptr(), stream)
-        torch.cuda.synchronize()
-        if i >= 10:
-            lat.append((time.perf_counter() - t1) * 1e3)
-    p50 = float(np.median(lat))
     model.close()
+    del model
+
+    p50 = None
+    if not args.no_latency:
+        # config 2: batch 1, seq 128, no padding; p50 latency of a hipGraph replay
+        lm = sj.Model(w, cfg, precision=sj.SJH_PREC_BF16, use_graphs=True)
+        rng = np.random.default_rng(7)
+        ids2 = rng.integers(0, cfg["vocab_size"], size=128).astype(np.int32)
+        d_ids2 = torch.from_numpy(ids2).cuda()
+        d_out2 = torch.empty((128, D), dtype=torch.float32, device="cuda")
+        l2 = np.array([128], np.int32)
+        lat = []
+        for i in range(60):
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            lm.encode_device(d_ids2.data_ptr(), l2, d_out2.data_ptr(), stream)
+            torch.cuda.synchronize()
+            if i >= 10:
+                lat.append((time.perf_counter() - t1) * 1e3)
+        p50 = round(float(np.median(lat)), 4)
+        lm.close()
 
     cpu = None if args.no_cpu else cpu_baseline(w, rl, enc, ids, mask, lens, NL)
     out = {
@@ -170,18 +193,20 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "gemm_bf16_mfma_kernel (QKV+RoPE, Wo+res, Wi+GEGLU, Wo2+res)",
+                     "kernel": "gemm_bf16_dma_kernel (QKV+RoPE, Wo+res, Wi+GEGLU, Wo2+res)",
                      "launches_per_step": gemm_launches // args.steps,
                      "flops_per_launch": flops_per_launch,
                      "avg_launch_us": round(avg_launch_s * 1e6, 3)},
         "attention_mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
         "attention_tflops": round(attn_tflops, 2),
-        "p50_latency_b1_ms": round(p50, 4),
+        "p50_latency_b1_ms": p50,
         "padded_tokens_per_s": round(B * S * args.steps / elapsed, 1),
         "kernel_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in sorted(prof.items())},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
 
 
 if __name__ == "__main__":

@@ -162,6 +162,15 @@ int sjh_gemm_geglu(const void* A, const void* Wi, void* C, int32_t M, int32_t F,
 int sjh_gemm_residual(const void* A, const void* W, float* X, int32_t M, int32_t D, int32_t K,
                       int32_t dtype, sjh_stream_t stream);
 
+/* sj_gemm followed by sj_rope (cuda/fast.cpp:183-190 runs them back to back;
+ * src/model.cpp:355-365 on the CPU): qkv[M, 3*H*Dh] = A[M,K] . Wqkv[3*H*Dh, K]^T
+ * with rotate-half RoPE applied to the q and k heads of each row, row m at
+ * position pos[m] (device int32 [M], clamped to [0, max_pos)); cos/sin fp32
+ * [max_pos, Dh/2]. */
+int sjh_gemm_qkv_rope(const void* A, const void* Wqkv, void* qkv, const int32_t* pos,
+                      const float* cos_t, const float* sin_t, int32_t max_pos, int32_t M,
+                      int32_t H, int32_t Dh, int32_t K, int32_t dtype, sjh_stream_t stream);
+
 /* sj_add_ln (cuda/kernels.cu:243-254): if residual, X += R (R of dtype);
  * Y = LN(X) * W (+ B if bias), Y of dtype.  X fp32 [M, D]. */
 int sjh_add_ln(float* X, const void* R, const float* W, const float* B, void* Y, int32_t M,

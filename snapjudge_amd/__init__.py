@@ -81,6 +81,9 @@ _SIGS = {
                                  C.c_int32, C.c_int32, C.c_void_p]),
     "sjh_gemm_residual": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                     C.c_int32, C.c_int32, C.c_void_p]),
+    "sjh_gemm_qkv_rope": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                    C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                    C.c_int32, C.c_int32, C.c_void_p]),
     "sjh_add_ln": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                              C.c_int32, C.c_int32, C.c_float, C.c_int32, C.c_int32, C.c_int32,
                              C.c_void_p]),

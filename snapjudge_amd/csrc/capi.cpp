@@ -225,6 +225,37 @@ int sjh_gemm_residual(const void* A, const void* W, float* X, int32_t M, int32_t
   });
 }
 
+int sjh_gemm_qkv_rope(const void* A, const void* Wqkv, void* qkv, const int32_t* pos,
+                      const float* cos_t, const float* sin_t, int32_t max_pos, int32_t M,
+                      int32_t H, int32_t Dh, int32_t K, int32_t dtype, sjh_stream_t stream) {
+  return guarded([&] {
+    check_dtype(dtype);
+    if (H <= 0 || Dh <= 0 || Dh % 2 != 0) sjh::fail("gemm_qkv_rope: bad head shape");
+    if (!pos || !cos_t || !sin_t) sjh::fail("gemm_qkv_rope: null positions or tables");
+    if (max_pos <= 0) sjh::fail("gemm_qkv_rope: max_pos must be positive");
+    sjh::GemmArgs g;
+    g.A = A;
+    g.lda = K;
+    g.W = Wqkv;
+    g.ldw = K;
+    g.M = M;
+    g.N = 3 * H * Dh;
+    g.K = K;
+    g.in_dtype = dtype;
+    g.epi = sjh::EPI_ROPE;
+    g.out = qkv;
+    g.ldo = 3 * H * Dh;
+    g.out_dtype = dtype;
+    g.pos = pos;
+    g.rope_cos = cos_t;
+    g.rope_sin = sin_t;
+    g.rope_rows = max_pos;
+    g.rope_dim = H * Dh;
+    g.head_dim = Dh;
+    sjh::launch_gemm(g, as_stream(stream));
+  });
+}
+
 int sjh_add_ln(float* X, const void* R, const float* W, const float* B, void* Y, int32_t M,
                int32_t D, float eps, int32_t residual, int32_t bias, int32_t dtype,
                sjh_stream_t stream) {

@@ -479,6 +479,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.pos = tok_pos_.as<int>();
       g.rope_cos = (ly.sliding ? rope_cos_slide_ : rope_cos_full_).as<float>();
       g.rope_sin = (ly.sliding ? rope_sin_slide_ : rope_sin_full_).as<float>();
+      g.rope_rows = max_pos_;
       g.rope_dim = D;
       g.head_dim = Dh_;
       gemm("gemm_qkv_rope", g, st);

@@ -1,13 +1,12 @@
 // gemm.hip -- projection GEMMs for gfx950: out[M, N] = epi(A[M, K] . W[N, K]^T).
 //
-// Fast path (bf16 in, fp32 accumulate): v_mfma_f32_32x32x16_bf16 on
-// 128x128x64 workgroup tiles.  256 threads = 4 waves in a 2x2 grid, each wave
-// owning a 64x64 sub-tile (2x2 MFMA blocks).  A and W tiles are staged in LDS
-// with a 16-byte row pad (double buffered; the next tile's global loads are in
-// flight while the current one feeds the MFMAs).  After the K loop the fp32
-// accumulators are staged in LDS once more so that the epilogue -- bias,
-// GELU/ReLU, residual add into the fp32 stream, RoPE on q/k, GEGLU -- works
-// on whole rows with coalesced stores.
+// Fast path (bf16 in, fp32 accumulate): v_mfma_f32_32x32x16_bf16 on block
+// tiles of up to 256x256 (16 waves of 64x64 for the throughput shapes).  A
+// and W tiles move from HBM into an LDS ring with direct-to-LDS loads
+// (global_load_lds_dwordx4, no register staging), XOR-swizzled so that the
+// MFMA operand reads are free of bank conflicts.  The epilogue -- bias,
+// GELU/ReLU, residual add into the fp32 stream, RoPE on q/k, GEGLU -- works on
+// the accumulators in registers, and the tile order is XCD-aware.
 //
 // Generic path (any shape, fp32 or bf16): 64x64x16 LDS tiles with 4x4 FMA
 // micro-tiles per thread and the same LDS-staged epilogue.  It serves the fp32
@@ -55,16 +54,16 @@ __device__ __forceinline__ void tile_epilogue(const float* Cs, int ldcs, int m0,
       if (n < 2 * g.rope_dim) {
         const int hd = g.head_dim, half = hd >> 1;
         const int dd = n % hd;
-        const int64_t p = g.pos[m];
+        const int64_t p = min(max(g.pos[m], 0), g.rope_rows - 1);
         if (dd < half) {
           const float x1 = Cs[r * ldcs + c + half];
           const float cs = g.rope_cos[p * half + dd], sn = g.rope_sin[p * half + dd];
-          v = v * cs - x1 * sn;
+          v = rope_lo(v, x1, cs, sn);
         } else {
           const int d2 = dd - half;
           const float x0 = Cs[r * ldcs + c - half];
           const float cs = g.rope_cos[p * half + d2], sn = g.rope_sin[p * half + d2];
-          v = v * cs + x0 * sn;
+          v = rope_hi(x0, v, cs, sn);
         }
       }
     } else {
@@ -93,115 +92,356 @@ __device__ __forceinline__ int64_t w_row(const GemmArgs g, int tile_n, int i) {
 }
 
 // ------------------------------------------------------------------ MFMA bf16
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kLdsK = kBK + 8;  // padded LDS row (elements): 144 B
-constexpr int kStageElems = (kBM + kBN) * kLdsK;
-constexpr int kLdsBytes = 2 * kStageElems * 2;  // two stages of bf16
-constexpr int kLdc = kBN + 4;
-static_assert(kBM * kLdc * 4 <= kLdsBytes, "epilogue tile must fit the staging LDS");
+//
+// Block tile BM x BN x 64 with WGM x WGN waves; each wave owns a
+// (BM/WGM) x (BN/WGN) sub-tile made of TI x TJ blocks of
+// v_mfma_f32_32x32x16_bf16.  Accumulator layout of one 32x32 block: lane l
+// holds column l % 32 and rows 8*(e/4) + 4*(l/32) + e%4, e = 0..15.
+//
+// The epilogue runs on the accumulators in registers:
+//   STORE  bias + GELU/ReLU, one element per (lane, e);
+//   RESID  X += acc (+ bias) on the fp32 residual stream;
+//   ROPE   head_dim 64: the two halves of a head (columns d and d + 32) are
+//          the same lane and register in blocks j and j + 1, so rotate-half
+//          needs no data movement;
+//   GEGLU  the block's W rows are arranged so that wave column wn's first
+//          TJ/2 blocks are input rows and its last TJ/2 blocks the gate rows
+//          of the same outputs: out = gelu(acc[j]) * acc[j + TJ/2].
+constexpr int kBK = 64;  // K must be a multiple of this for the MFMA path
 
-template <typename OutT>
-__global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
-  bf16_t* stage = reinterpret_cast<bf16_t*>(smem);
+// Workgroups are handed to the 8 XCDs round-robin (id % 8).  Renumber them
+// so that each XCD receives a contiguous run of tiles, N fastest: the tiles
+// of one A row panel then share that XCD's L2.
+__device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
+  const int xcd = bid & 7, local = bid >> 3;
+  const int per = nblocks >> 3, rem = nblocks & 7;
+  return xcd * per + min(xcd, rem) + local;
+}
 
-  const int tile_n = blockIdx.x, tile_m = blockIdx.y;
-  const int m0 = tile_m * kBM;
+// W row staged at tile row i (0 <= i < BN) of column tile tile_n.
+template <int BN, int WN, int EPI>
+__device__ __forceinline__ int64_t mfma_w_row(const GemmArgs& g, int tile_n, int i) {
+  if constexpr (EPI == EPI_GEGLU) {
+    constexpr int half = WN / 2;
+    const int wn = i / WN, within = i - wn * WN;
+    int o = tile_n * (BN / 2) + wn * half + (within < half ? within : within - half);
+    o = o < g.N ? o : g.N - 1;
+    return within < half ? o : static_cast<int64_t>(g.N) + o;
+  } else {
+    const int n = tile_n * BN + i;
+    return n < g.N ? n : g.N - 1;
+  }
+}
+
+// Epilogue on the accumulators in registers (see the comment above).
+template <int BM, int BN, int WM, int WN, int TI, int TJ, int EPI, typename OutT>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int m0,
+                                              int tile_n, int wm, int wn, int l32, int hb) {
+  const int row_base = m0 + wm * WM + 4 * hb;
+  if constexpr (EPI == EPI_GEGLU) {
+    OutT* out = static_cast<OutT*>(g.out);
+    const int c0 = tile_n * (BN / 2) + wn * (WN / 2) + l32;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
+        if (m >= g.M) continue;
+        OutT* orow = out + static_cast<int64_t>(m) * g.ldo;
+#pragma unroll
+        for (int j = 0; j < TJ / 2; ++j) {
+          const int col = c0 + j * 32;
+          if (col < g.N) store_f32(orow + col, gelu_erf(acc[i][j][e]) * acc[i][j + TJ / 2][e]);
+        }
+      }
+  } else if constexpr (EPI == EPI_RESID) {
+    const int c0 = tile_n * BN + wn * WN + l32;
+    float bv[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) bv[j] = (g.bias && c0 + j * 32 < g.N) ? g.bias[c0 + j * 32] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
+        if (m >= g.M) continue;
+        float* xrow = g.X + static_cast<int64_t>(m) * g.ldx;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          const int col = c0 + j * 32;
+          if (col < g.N) xrow[col] += acc[i][j][e] + bv[j];
+        }
+      }
+  } else if constexpr (EPI == EPI_ROPE) {
+    // head_dim 64 (checked by the launcher): block j holds dims [0, 32) of a
+    // head when j is even and dims [32, 64) when odd; its partner is j ^ 1.
+    static_assert(TJ % 2 == 0, "RoPE pairs need an even number of column blocks");
+    OutT* out = static_cast<OutT*>(g.out);
+    const int c0 = tile_n * BN + wn * WN;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
+        if (m >= g.M) continue;
+        OutT* orow = out + static_cast<int64_t>(m) * g.ldo;
+        const int p = min(max(g.pos[m], 0), g.rope_rows - 1);
+        const int64_t tb = static_cast<int64_t>(p) * 32 + l32;
+        const float cs = g.rope_cos[tb], sn = g.rope_sin[tb];
+#pragma unroll
+        for (int j = 0; j < TJ; j += 2) {
+          const int col = c0 + j * 32 + l32;
+          if (col >= g.N) continue;
+          float x0 = acc[i][j][e], x1 = acc[i][j + 1][e];
+          if (c0 + j * 32 < 2 * g.rope_dim) {
+            const float r0 = rope_lo(x0, x1, cs, sn);
+            const float r1 = rope_hi(x0, x1, cs, sn);
+            x0 = r0;
+            x1 = r1;
+          }
+          store_f32(orow + col, x0);
+          if (col + 32 < g.N) store_f32(orow + col + 32, x1);
+        }
+      }
+  } else {
+    OutT* out = static_cast<OutT*>(g.out);
+    const int c0 = tile_n * BN + wn * WN + l32;
+    float bv[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) bv[j] = (g.bias && c0 + j * 32 < g.N) ? g.bias[c0 + j * 32] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
+        if (m >= g.M) continue;
+        OutT* orow = out + static_cast<int64_t>(m) * g.ldo;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          const int col = c0 + j * 32;
+          if (col >= g.N) continue;
+          float v = acc[i][j][e] + bv[j];
+          if (g.act == 1)
+            v = gelu_erf(v);
+          else if (g.act == 2)
+            v = fmaxf(v, 0.f);
+          store_f32(orow + col, v);
+        }
+      }
+  }
+}
+
+// ---- direct-to-LDS variant -------------------------------------------------
+// Tiles move from HBM to LDS with global_load_lds_dwordx4 (no VGPR staging):
+// lane l of an instruction writes its 16 bytes at LDS address base + 16*l, so
+// one instruction fills 1 KB of unpadded tile rows (8 rows of a 64-deep K
+// step, 16 rows of a 32-deep one).  Bank conflicts on the MFMA operand reads
+// are avoided by an XOR swizzle of the 16-byte chunks within a row.  NS
+// stages form a ring; the loads for stage kt + NS - 1 are issued right after
+// the barrier that opens iteration kt, so NS - 1 stages are in flight while
+// stage kt is consumed.
+template <int BM, int BN, int WGM, int WGN, int NS, int BK>
+struct DTile {
+  static constexpr int NW = WGM * WGN;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
+  static constexpr int TI = WM / 32, TJ = WN / 32;
+  static constexpr int RB = BK * 2;                // bytes per tile row
+  static constexpr int CPR = BK / 8;               // 16-byte chunks per row
+  static constexpr int RPI = 1024 / RB;            // rows per load instruction
+  static constexpr int GROUPS = (BM + BN) / RPI;   // load instructions per stage
+  static constexpr int G = GROUPS / NW;            // ... per wave
+  static constexpr int STAGE_BYTES = (BM + BN) * RB;
+  static_assert(BK == 32 || BK == 64, "K step is 32 or 64");
+  static_assert(G * NW == GROUPS && BM % RPI == 0, "row groups must split evenly over waves");
+  static_assert(TI >= 1 && TJ >= 1, "tile too small");
+  static_assert(NS >= 2 && NS * STAGE_BYTES <= 160 * 1024, "LDS ring does not fit");
+  static_assert(G * (NS - 2) <= 63, "vmcnt range");
+  // chunk position of logical chunk c in tile row r is c ^ swz(r).  The LDS
+  // serves a 16-byte read for 16 lanes at a time across 64 four-byte banks;
+  // 16 consecutive rows at one logical chunk then land in 16 distinct
+  // 16-byte bank groups.
+  static __device__ __forceinline__ int swz(int r) {
+    return BK == 64 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+  }
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt immediate");
+  if constexpr (N == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs g) {
+  using TT = DTile<BM, BN, WGM, WGN, NS, BK>;
+  constexpr int TI = TT::TI, TJ = TT::TJ, G = TT::G, RB = TT::RB, CPR = TT::CPR;
+  constexpr int KS = BK / 16;  // MFMA K steps per stage
+  extern __shared__ __attribute__((aligned(16))) char dsmem[];
+
+  const int tiles_n = EPI == EPI_GEGLU ? g.N / (BN / 2) : (g.N + BN - 1) / BN;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int tile_m = tile / tiles_n, tile_n = tile - tile_m * tiles_n;
+  const int m0 = tile_m * BM;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int l32 = lane & 31, hb = lane >> 5;
 
   const bf16_t* A = static_cast<const bf16_t*>(g.A);
   const bf16_t* W = static_cast<const bf16_t*>(g.W);
 
-  // global -> register assignment: 16-byte chunks, 8 per 64-element row; a
-  // thread moves rows r0 + 32*i (i < 4) at k-chunk kc of both operands.
-  constexpr int kChunks = kBM * kBK / 8 / 256;  // 4 (A) and 4 (W)
-  static_assert(kBM == kBN, "A and W tiles share the chunk assignment");
-  const int r0 = tid >> 3, kc = tid & 7;
-  int64_t a_off[kChunks], w_off[kChunks];
+  // this wave's row groups: q = wave + NW * i; lane moves tile row
+  // RPI * q + lane / CPR into chunk slot lane % CPR, reading the logical
+  // chunk that the swizzle maps there
+  const bf16_t* src[G];
+  const int lrow = lane / CPR, cslot = lane % CPR;
 #pragma unroll
-  for (int i = 0; i < kChunks; ++i) {
-    const int row = r0 + 32 * i;
-    a_off[i] = static_cast<int64_t>(min(m0 + row, g.M - 1)) * g.lda + kc * 8;
-    w_off[i] = w_row<kBN>(g, tile_n, row) * g.ldw + kc * 8;
+  for (int i = 0; i < G; ++i) {
+    const int r = TT::RPI * (wave + TT::NW * i) + lrow;
+    const int gchunk = cslot ^ TT::swz(r);
+    if (r < BM)
+      src[i] = A + static_cast<int64_t>(min(m0 + r, g.M - 1)) * g.lda + gchunk * 8;
+    else
+      src[i] = W + mfma_w_row<BN, TT::WN, EPI>(g, tile_n, r - BM) * g.ldw + gchunk * 8;
   }
-  const int lds_off = r0 * kLdsK + kc * 8;  // + 32*i rows
-
-  u32x4_t ra[kChunks], rw[kChunks];
-  static_assert(kChunks == 4, "the load/store macros below move 4 chunks per operand");
-#define SJH_LD1(i, k0)                                                   \
-  ra[i] = *reinterpret_cast<const u32x4_t*>(A + a_off[i] + (k0));          \
-  rw[i] = *reinterpret_cast<const u32x4_t*>(W + w_off[i] + (k0));
-#define SJH_GEMM_LOAD(k0) \
-  SJH_LD1(0, k0) SJH_LD1(1, k0) SJH_LD1(2, k0) SJH_LD1(3, k0)
-#define SJH_ST1(i, buf)                                                                     \
-  *reinterpret_cast<u32x4_t*>(stage + (buf) * kStageElems + lds_off + 32 * (i) * kLdsK) = ra[i]; \
-  *reinterpret_cast<u32x4_t*>(stage + (buf) * kStageElems + kBM * kLdsK + lds_off +             \
-                            32 * (i) * kLdsK) = rw[i];
-#define SJH_GEMM_STORE(buf) \
-  SJH_ST1(0, buf) SJH_ST1(1, buf) SJH_ST1(2, buf) SJH_ST1(3, buf)
-
-  f32x16_t acc[2][2];
+  auto issue = [&](int kt, int buf) {
+    char* base = dsmem + buf * TT::STAGE_BYTES;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < G; ++i)
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void*>(src[i] + kt * BK),
+          (__attribute__((address_space(3))) void*)(base + (wave + TT::NW * i) * 1024), 16, 0,
+          0);
+  };
+
+  f32x16_t acc[TI][TJ];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  SJH_GEMM_LOAD(0)
-  SJH_GEMM_STORE(0)
-  __syncthreads();
-  const int nk = g.K / kBK;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      const int kn = (kt + 1) * kBK;
-      SJH_GEMM_LOAD(kn)
-    }
-    const bf16_t* As = stage + cur * kStageElems + (wm * 64 + l32) * kLdsK + hb * 8;
-    const bf16_t* Ws = stage + cur * kStageElems + kBM * kLdsK + (wn * 64 + l32) * kLdsK + hb * 8;
+  const int nk = g.K / BK;
 #pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      bf16x8_t af[2], bw[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t*>(As + i * 32 * kLdsK + s * 16);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bw[j] = *reinterpret_cast<const bf16x8_t*>(Ws + j * 32 * kLdsK + s * 16);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bw[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) {
-      SJH_GEMM_STORE(cur ^ 1)
-    }
-    __syncthreads();
-  }
-#undef SJH_LD1
-#undef SJH_ST1
-#undef SJH_GEMM_LOAD
-#undef SJH_GEMM_STORE
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(s, s);
 
-  // accumulator layout of a 32x32 block: lane l holds column l%32 and rows
-  // 8*(e/4) + 4*(l/32) + e%4 for e = 0..15.
-  float* Cs = reinterpret_cast<float*>(smem);
+  // operand rows of this lane; tile bases are multiples of 32, so the
+  // swizzle key of row base + l32 is that of l32
+  const int xr = TT::swz(l32);
+  const int a_row0 = (wm * TT::WM + l32) * RB, w_row0 = (BM + wn * TT::WN + l32) * RB;
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + NS - 2 < nk)
+      wait_vmcnt<G * (NS - 2)>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
+    const char* sb = dsmem + (kt % NS) * TT::STAGE_BYTES;
+    // operand fragments double-buffered across the K steps so the LDS reads
+    // of step s + 1 are in flight during the MFMAs of step s
+    bf16x8_t af[2][TI], bw[2][TJ];
+    auto frag = [&](int s, int buf) {
+      const int coff = ((2 * s + hb) ^ xr) * 16;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TI; ++i)
+        af[buf][i] = *reinterpret_cast<const bf16x8_t*>(sb + a_row0 + i * 32 * RB + coff);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < TJ; ++j)
+        bw[buf][j] = *reinterpret_cast<const bf16x8_t*>(sb + w_row0 + j * 32 * RB + coff);
+    };
+    frag(0, 0);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * hb + (e & 3);
-        const int col = wn * 64 + j * 32 + l32;
-        Cs[row * kLdc + col] = acc[i][j][e];
+    for (int s = 0; s < KS; ++s) {
+      if (s + 1 < KS) frag(s + 1, (s + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s & 1][i], bw[s & 1][j],
+                                                               acc[i][j], 0, 0, 0);
+    }
+    // Pin the schedule: the reads of step 0, then for each step its MFMAs
+    // interleaved one-for-one with the reads of the next step (mask 0x008 =
+    // MFMA, 0x100 = LDS read).
+#pragma unroll
+    for (int r = 0; r < TI + TJ; ++r) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int k = 0; k < TI * TJ; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (s + 1 < KS && k < TI + TJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-  __syncthreads();
-  tile_epilogue<kBM, kBN, 256, OutT>(Cs, kLdc, m0, tile_n, g);
+      if (s + 1 < KS) {
+#pragma unroll
+        for (int k = TI * TJ; k < TI + TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+  }
+
+  gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tile_n, wm, wn, l32, hb);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
+void launch_mfma_kernel(const GemmArgs& g, dim3 grid, hipStream_t st) {
+  constexpr int lds = NS * DTile<BM, BN, WGM, WGN, NS, BK>::STAGE_BYTES;
+  auto kern = gemm_bf16_dma_kernel<BM, BN, WGM, WGN, NS, BK, EPI, OutT>;
+  static bool attr_set = false;  // per instantiation; the attribute is per function
+  if (!attr_set) {
+    hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+              "gemm: LDS attribute");
+    attr_set = true;
+  }
+  kern<<<grid, 64 * WGM * WGN, lds, st>>>(g);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI>
+void launch_mfma_tile(const GemmArgs& g, hipStream_t st) {
+  const int tiles_n = EPI == EPI_GEGLU ? g.N / (BN / 2) : (g.N + BN - 1) / BN;
+  const int64_t tiles = static_cast<int64_t>(tiles_n) * ((g.M + BM - 1) / BM);
+  require(tiles < (int64_t{1} << 31), "gemm: too many tiles");
+  dim3 grid(static_cast<unsigned>(tiles));
+  if (g.out_dtype == DT_BF16 || EPI == EPI_RESID)
+    launch_mfma_kernel<BM, BN, WGM, WGN, NS, BK, EPI, bf16_t>(g, grid, st);
+  else
+    launch_mfma_kernel<BM, BN, WGM, WGN, NS, BK, EPI, float>(g, grid, st);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int BK>
+void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
+  switch (g.epi) {
+    case EPI_STORE: launch_mfma_tile<BM, BN, WGM, WGN, NS, BK, EPI_STORE>(g, st); break;
+    case EPI_RESID: launch_mfma_tile<BM, BN, WGM, WGN, NS, BK, EPI_RESID>(g, st); break;
+    case EPI_ROPE: launch_mfma_tile<BM, BN, WGM, WGN, NS, BK, EPI_ROPE>(g, st); break;
+    default: launch_mfma_tile<BM, BN, WGM, WGN, NS, BK, EPI_GEGLU>(g, st); break;
+  }
+}
+
+#ifndef SJH_GEMM_BIG
+#define SJH_GEMM_BIG 256, 256, 4, 4, 2, 64
+#endif
+#ifndef SJH_GEMM_MID
+#define SJH_GEMM_MID 128, 128, 2, 2, 2, 64
+#endif
+
+// Tile shapes by row count (BM, BN, wave grid, ring stages, K step): 256x256
+// with 16 waves of 64x64 (4 waves per SIMD hide the LDS and MFMA latencies)
+// for the throughput shapes; 128x128 with 4 waves for mid-size batches;
+// 64x128 with 4 waves of 32x64 for short ones (batch-1 latency), where more
+// workgroups are needed to spread the weight reads over the CUs.
+void launch_mfma(const GemmArgs& g, hipStream_t st) {
+  if (g.M >= 4096 && (g.epi != EPI_GEGLU || g.N % 128 == 0))
+    launch_mfma_epi<SJH_GEMM_BIG>(g, st);
+  else if (g.M >= 1024)
+    launch_mfma_epi<SJH_GEMM_MID>(g, st);
+  else
+    launch_mfma_epi<64, 128, 2, 2, 2, 64>(g, st);
 }
 
 // ------------------------------------------------------------------ generic
@@ -295,7 +535,8 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
       break;
     case EPI_ROPE:
       require(g.out && g.ldo >= g.N, "gemm: ROPE needs out with ldo >= N");
-      require(g.pos && g.rope_cos && g.rope_sin, "gemm: ROPE needs positions and tables");
+      require(g.pos && g.rope_cos && g.rope_sin && g.rope_rows > 0,
+              "gemm: ROPE needs positions and tables");
       require(g.head_dim > 0 && g.head_dim % 2 == 0 && g.rope_dim % g.head_dim == 0 &&
                   2 * g.rope_dim <= g.N,
               "gemm: ROPE head layout");
@@ -308,18 +549,12 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
   }
   const bool mfma = g.in_dtype == DT_BF16 && g.K % kBK == 0 && g.lda % 8 == 0 &&
                     g.ldw % 8 == 0 && aligned16(g.A) && aligned16(g.W) &&
-                    (g.epi != EPI_ROPE || kBN % g.head_dim == 0) &&
-                    (g.epi != EPI_GEGLU || g.N % (kBN / 2) == 0);
+                    (g.epi != EPI_ROPE || g.head_dim == 64) &&
+                    (g.epi != EPI_GEGLU || g.N % 64 == 0);
   if (g.epi == EPI_ROPE && !mfma)
     require(gBN % g.head_dim == 0, "gemm: ROPE epilogue needs head_dim dividing 64");
   if (mfma) {
-    const int ntiles =
-        g.epi == EPI_GEGLU ? g.N / (kBN / 2) : (g.N + kBN - 1) / kBN;
-    dim3 grid(ntiles, (g.M + kBM - 1) / kBM), block(256);
-    if (g.out_dtype == DT_BF16)
-      gemm_bf16_mfma_kernel<bf16_t><<<grid, block, 0, st>>>(g);
-    else
-      gemm_bf16_mfma_kernel<float><<<grid, block, 0, st>>>(g);
+    launch_mfma(g, st);
     check_launch("gemm_bf16_mfma");
     return;
   }

@@ -129,8 +129,8 @@ __global__ void rope_kernel(T* qkv, int64_t M, int64_t ld, const int* pos, int L
   const float x0 = load_f32(x + d), x1 = load_f32(x + d + half);
   const float c = cos_t[static_cast<int64_t>(p) * half + d];
   const float s = sin_t[static_cast<int64_t>(p) * half + d];
-  store_f32(x + d, x0 * c - x1 * s);
-  store_f32(x + d + half, x1 * c + x0 * s);
+  store_f32(x + d, rope_lo(x0, x1, c, s));
+  store_f32(x + d + half, rope_hi(x0, x1, c, s));
 }
 
 __global__ void token_index_kernel(const int* seq_start, const int* rows, int* tok_pos,

@@ -36,6 +36,20 @@ __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654757f));
 }
 
+// Rotate-half RoPE on one pair (x0 = dim d, x1 = dim d + Dh/2), as
+// src/tensor.cpp:257-279: each product rounded to float, then the sum.
+// Contraction into a fused multiply-add is switched off here so that every
+// kernel that inlines these (whatever its register schedule) rounds the same
+// way.
+__device__ __forceinline__ float rope_lo(float x0, float x1, float c, float s) {
+#pragma clang fp contract(off)
+  return x0 * c - x1 * s;
+}
+__device__ __forceinline__ float rope_hi(float x0, float x1, float c, float s) {
+#pragma clang fp contract(off)
+  return x1 * c + x0 * s;
+}
+
 template <typename T>
 __device__ __forceinline__ float load_f32(const T* p);
 template <>

@@ -39,7 +39,8 @@ struct GemmArgs {
   int64_t ldx = 0;
   const int* pos = nullptr;  // ROPE: position of each row
   const float* rope_cos = nullptr;
-  const float* rope_sin = nullptr;  // [max_pos, head_dim/2]
+  const float* rope_sin = nullptr;  // [rope_rows, head_dim/2]
+  int rope_rows = 0;                // positions are clamped to [0, rope_rows)
   int rope_dim = 0;                 // D: columns [0, 2D) are q and k
   int head_dim = 0;
 };

@@ -215,3 +215,56 @@ def test_embed_ln(orc, dtype):
     call(sj.lib().sjh_embed_ln, P(T), P(I), P(Wt), P(X), M, D, C.c_float(1e-5), cdt, stream())
     want = orc.layer_norm(table[ids], w, None, 1e-5)
     assert float(np.abs(host(X) - want).max()) <= 1e-5 * max(1.0, float(np.abs(want).max()))
+
+
+@pytest.mark.parametrize("M", [300, 1500, 5000])
+def test_gemm_qkv_rope(orc, M):
+    # fused QKV projection + RoPE (the reference runs gemm_nt then rope_inplace,
+    # src/model.cpp:355-365); row r at position r % L
+    print(f"gemm_qkv_rope M={M}", flush=True)
+    rng = np.random.default_rng(M)
+    H, Dh, K, L = 12, 64, 768, 512
+    a, w = rnd(rng, (M, K)), rnd(rng, (3 * H * Dh, K), 0.05)
+    c, s = orc.rope_table(160000.0, L, Dh)
+    pos = (np.arange(M) % L).astype(np.int32)
+    A, W = dev(a, torch.bfloat16), dev(w, torch.bfloat16)
+    Ct, St = dev(c, torch.float32), dev(s, torch.float32)
+    Pt = torch.from_numpy(pos).cuda()
+    Q = torch.empty((M, 3 * H * Dh), dtype=torch.bfloat16, device="cuda")
+    call(sj.lib().sjh_gemm_qkv_rope, P(A), P(W), P(Q), P(Pt), P(Ct), P(St), L, M, H, Dh, K, BF,
+         stream())
+    want = orc.rope_inplace(orc.gemm_nt(a, w), c, s, L, H, Dh)
+    assert rel_err(host(Q), want) < 8e-3
+
+
+def test_gemm_tile_shape_invariance():
+    # the tile shape is chosen from M; a row's result must not depend on it
+    # (bit-identical for every epilogue)
+    rng = np.random.default_rng(5)
+    K, H, Dh, L = 768, 12, 64, 512
+    Mb, Ms = 5000, 300
+    a = rnd(rng, (Mb, K))
+    A = dev(a, torch.bfloat16)
+    c, s = (np.cos(np.arange(L * 32).reshape(L, 32) * 1e-3).astype(np.float32),
+            np.sin(np.arange(L * 32).reshape(L, 32) * 1e-3).astype(np.float32))
+    Ct, St = dev(c, torch.float32), dev(s, torch.float32)
+    Pt = torch.from_numpy((np.arange(Mb) % L).astype(np.int32)).cuda()
+    for kind, nw, n in (("store", 768, 768), ("geglu", 2304, 1152), ("resid", 768, 768),
+                        ("rope", 2304, 2304)):
+        W = dev(rnd(rng, (nw, K), 0.05), torch.bfloat16)
+        res = []
+        for M in (Mb, 1500, Ms):
+            odt = torch.float32 if kind == "resid" else torch.bfloat16
+            O = torch.zeros((M, n), dtype=odt, device="cuda")
+            if kind == "store":
+                call(sj.lib().sjh_gemm, P(A), P(W), None, P(O), M, n, K, 1, BF, stream())
+            elif kind == "geglu":
+                call(sj.lib().sjh_gemm_geglu, P(A), P(W), P(O), M, n, K, BF, stream())
+            elif kind == "resid":
+                call(sj.lib().sjh_gemm_residual, P(A), P(W), P(O), M, n, K, BF, stream())
+            else:
+                call(sj.lib().sjh_gemm_qkv_rope, P(A), P(W), P(O), P(Pt), P(Ct), P(St), L, M, H,
+                     Dh, K, BF, stream())
+            res.append(host(O)[:Ms])
+        print(kind, [int((r != res[0]).sum()) for r in res], flush=True)
+        assert all(np.array_equal(r, res[0]) for r in res), kind
