@@ -20,9 +20,12 @@ LIB = os.path.join(HERE, "libsnapjudge_hip.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32.
+# -amdgpu-mfma-vgpr-form: MFMA results go to ordinary VGPRs, so the softmax
+# and epilogue math on them needs no AGPR round trips.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I" + CSRC, "-I" + os.path.join(ROOT, "include"),
 ]
 

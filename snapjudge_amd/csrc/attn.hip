@@ -1,15 +1,18 @@
 // attn.hip -- non-causal varlen flash attention for gfx950.
 //
 // Fast path (bf16, head_dim 64): one workgroup = (sequence, head, 128
-// queries); 4 waves own 32 queries each.  Key/value tiles of 64 rows are
-// staged in LDS (K row-major, V transposed to [dim][key]).  Per tile a wave
-// computes S^T = K . Q^T with v_mfma_f32_32x32x16_bf16 (the query is the MFMA
-// column, so each lane owns one query and 32 of the tile's keys), does the
-// online-softmax update in registers (row max over its own values plus one
-// cross-half exchange; exp2 with the 1/sqrt(Dh)*log2(e) scale folded in), and
-// accumulates O^T += V^T . P^T.  The accumulator of S^T is already laid out
-// as the B operand of the second MFMA once the key order inside a 16-key
-// step is taken as the MFMA's k order, so P never leaves registers.
+// queries); 4 waves own 32 queries each.  Key/value tiles of 64 rows move
+// from HBM into a 3-stage LDS ring with direct-to-LDS loads, row-major and
+// XOR-swizzled.  Per tile a wave computes S^T = K . Q^T with
+// v_mfma_f32_32x32x16_bf16 (the query is the MFMA column, so each lane owns
+// one query and 32 of the tile's keys), does the online-softmax update in
+// registers (row max over its own values plus one cross-half exchange; exp2
+// with the 1/sqrt(Dh)*log2(e) scale folded in), and accumulates
+// O^T += V^T . P^T.  The accumulator of S^T is already laid out as the B
+// operand of the second MFMA once the key order inside a 16-key step is taken
+// as the MFMA's k order, so P never leaves registers; the V^T operand comes
+// straight from the row-major V tile through transposed LDS reads
+// (ds_read_b64_tr_b16).
 //
 // Generic path (fp32 or bf16, head_dim 8/16/32/64/128): one thread per query,
 // K/V tiles of 32 keys in LDS (broadcast reads), blocked online softmax with
@@ -18,6 +21,8 @@
 // Masking follows src/tensor.cpp:186-192: query i sees keys
 // [0, k_len) (full) or [max(0, i-w), min(k_len, i+w+1)) (window w).  A query
 // with no visible key yields zeros, as the reference does for len = 0.
+#include <type_traits>
+
 #include "sjh_common.hpp"
 #include "sjh_host.hpp"
 #include "sjh_kernels.hpp"
@@ -27,21 +32,43 @@ namespace sjh {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kQ = 128;   // queries per workgroup
-constexpr int kKey = 64;  // keys per tile
-constexpr int kLdK = 64 + 8;  // padded K row (elements): 144 B
-constexpr int kLdV = 64 + 8;  // padded V^T row (elements)
+constexpr int kQ = 128;     // queries per workgroup (4 waves x 32)
+constexpr int kKey = 64;    // keys per tile
+constexpr int kNS = 3;      // LDS ring stages
+constexpr float kLazy = 8.f;  // log2 headroom before the running max is raised
+constexpr int kStage = 2 * kKey * 128;  // bytes per stage: K tile then V tile, 64 x 128 B each
+
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((ext_vector_type(8))) short s16x8_t;
 
 __device__ __forceinline__ float wave_max32(float v) {
   // lanes l and l^32 hold the two halves of one query's keys
   return fmaxf(v, __shfl_xor(v, 32, 64));
 }
 
+// Chunk position of 16-byte chunk c of tile row r is c ^ kv_swz(r): 16
+// consecutive rows read at one logical chunk hit 16 distinct bank groups.
+__device__ __forceinline__ int kv_swz(int r) { return (r >> 1) & 7; }
+
+// LDS byte offset of element (row, col) of a 64 x 64 bf16 tile.
+__device__ __forceinline__ int kv_off(int row, int col) {
+  return row * 128 + (((col >> 3) ^ kv_swz(row)) << 4) + ((col & 7) << 1);
+}
+
+// Transposed 8-byte LDS read (ds_read_b64_tr_b16).  Within each 16-lane
+// group, if lane q + 4k addresses element (r0 + k, c0 + 4q) of a row-major
+// tile, lane i of the group receives elements (r0 + k, c0 + i), k = 0..3.
+__device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t*)(p));
+}
+
 __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kNS * kStage];
   const int b = blockIdx.z, h = blockIdx.y;
   const int qlen = a.q_len ? a.q_len[b] : a.uniform_L;
   const int q0 = blockIdx.x * kQ;
-  if (q0 >= qlen) return;
+  if (q0 >= qlen) return;  // uniform over the workgroup
   // keys never extend past the rows a sequence owns (a caller's k_len > L in
   // the padded layout is clamped rather than read out of bounds)
   const int klen = a.seq_start ? a.k_len[b] : max(0, min(a.k_len[b], a.uniform_L));
@@ -53,11 +80,9 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
   const bf16_t* K = static_cast<const bf16_t*>(a.k) + h * 64;
   const bf16_t* V = static_cast<const bf16_t*>(a.v) + h * 64;
 
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[kKey * kLdK];
-  __shared__ __attribute__((aligned(16))) bf16_t Vt[64 * kLdV];
-
   // this lane's query (clamped for the load; rows past q_len are not stored)
   const int qi = q0 + wave * 32 + l32;
+  const bool wave_active = q0 + wave * 32 < qlen;
   const int64_t qrow = row0 + min(qi, qlen - 1);
   bf16x8_t qf[4];
 #pragma unroll
@@ -71,6 +96,25 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
   }
   const int qlo = a.window > 0 ? max(0, qi - a.window) : 0;
   const int qhi = a.window > 0 ? min(klen, qi + a.window + 1) : klen;
+  const int ntiles = khi > klo ? (khi - klo + kKey - 1) / kKey : 0;
+
+  // DMA: a stage is 16 row groups of 8 rows x 128 B (groups 0-7 K, 8-15 V);
+  // wave w moves groups w, w + 4, w + 8, w + 12.  Lane l carries row
+  // 8 * (group % 8) + l / 8 and lands in chunk slot l % 8, so it reads the
+  // logical chunk (l % 8) ^ kv_swz(row).
+  const int lrow = lane >> 3, cslot = lane & 7;
+  auto issue = [&](int t, int buf) {
+    char* base = smem + buf * kStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int grp = wave + 4 * i;
+      const int r = 8 * (grp & 7) + lrow;
+      const int key = min(klo + t * kKey + r, klen - 1);
+      const bf16_t* src = (grp < 8 ? K + (row0 + key) * a.ld_k : V + (row0 + key) * a.ld_v) +
+                          ((cslot ^ kv_swz(r)) << 3);
+      load_lds16(src, base + grp * 1024);
+    }
+  };
 
   f32x16_t o[2];
 #pragma unroll
@@ -81,31 +125,36 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
   float m_i = -INFINITY, l_i = 0.f;
   const float c = a.scale * kLog2e;
 
-  for (int kt = klo; kt < khi; kt += kKey) {
-    // K tile: 64 keys x 64 dims, 16-byte chunks, 2 per thread.
+  // LDS offsets (within a stage) of this lane's operand reads, the same for
+  // every tile.  K fragments: row jb*32 + l32, dims 16*st + 8*hb + [0, 8).
+  // V^T fragments through transposed reads (see lds_read_tr): lane group
+  // g = lane / 16 covers dims 16 * (g % 2) + [0, 16) of a 32-dim block and
+  // keys 4 * (g / 2) + [0, 4) of an 8-key half step.
+  int koff[2][4], voff[2][2][2][2];
+  {
+    const int tq = lane & 3, tk = (lane >> 2) & 3, tg = lane >> 4;
+    const int tdim = 16 * (tg & 1) + 4 * tq;
+    const int tkey = 4 * (tg >> 1) + tk;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int ch = tid + 256 * i, r = ch >> 3, dc = ch & 7;
-      const int key = min(kt + r, klen - 1);
-      *reinterpret_cast<u32x4_t*>(Ks + r * kLdK + dc * 8) =
-          *reinterpret_cast<const u32x4_t*>(K + (row0 + key) * a.ld_k + dc * 8);
-    }
-    // V tile transposed: a thread takes two keys x 8 dims and writes 8 key pairs.
-    {
-      const int kp = tid >> 3, dc = tid & 7;
-      const int k0 = min(kt + 2 * kp, klen - 1), k1 = min(kt + 2 * kp + 1, klen - 1);
-      const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(V + (row0 + k0) * a.ld_v + dc * 8);
-      const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(V + (row0 + k1) * a.ld_v + dc * 8);
+    for (int jb = 0; jb < 2; ++jb) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        *reinterpret_cast<uint32_t*>(Vt + (dc * 8 + 2 * e) * kLdV + 2 * kp) =
-            (w0[e] & 0xffffu) | (w1[e] << 16);
-        *reinterpret_cast<uint32_t*>(Vt + (dc * 8 + 2 * e + 1) * kLdV + 2 * kp) =
-            (w0[e] >> 16) | (w1[e] & 0xffff0000u);
-      }
+      for (int st = 0; st < 4; ++st) koff[jb][st] = kv_off(jb * 32 + l32, 16 * st + 8 * hb);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int hl = 0; hl < 2; ++hl)
+            voff[jb][u][db][hl] =
+                kKey * 128 + kv_off(jb * 32 + 16 * u + 8 * hl + tkey, db * 32 + tdim);
     }
-    __syncthreads();
+  }
 
+  // One 64-key tile at key offset kt from the stage at sb.  MASK: apply the
+  // key range [qlo, qhi) (last tile, or a sliding window); interior tiles of
+  // full attention skip it.
+  auto tile = [&](auto mask_tag, const char* sb, int kt) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     // S^T[key][query] for keys kt + [0, 32) and kt + [32, 64)
     f32x16_t s[2];
 #pragma unroll
@@ -114,46 +163,58 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
       for (int e = 0; e < 16; ++e) s[jb][e] = 0.f;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const bf16x8_t kf =
-            *reinterpret_cast<const bf16x8_t*>(Ks + (jb * 32 + l32) * kLdK + 16 * st + 8 * hb);
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(sb + koff[jb][st]);
         s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[jb], 0, 0, 0);
       }
     }
-    // scale into the log2 domain, mask, tile max
-    const bool need_mask = (kt + kKey > klen) || a.window > 0;
+    if constexpr (MASK) {
+      // key of element (jb, e) is kt + 4*hb + 32*jb + 8*(e/4) + e%4
+      const int lo = qlo - kt - 4 * hb, hi = qhi - kt - 4 * hb;
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int k = 32 * jb + 8 * (e >> 2) + (e & 3);
+          s[jb][e] = (k < lo || k >= hi) ? -INFINITY : s[jb][e];
+        }
+    }
+    // Online softmax in the log2 domain (c = scale * log2 e).  A lane keeps
+    // its running max m_i unless the tile's max exceeds it by more than
+    // kLazy: p = 2^(s*c - m_i) then stays below 2^kLazy, the final 1/l
+    // normalisation uses the same m_i, so the result is exact while the
+    // rescale of O and l is skipped for most tiles.
     float tmax = -INFINITY;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float v = s[jb][e] * c;
-        if (need_mask) {
-          const int key = kt + jb * 32 + 8 * (e >> 2) + 4 * hb + (e & 3);
-          if (key < qlo || key >= qhi) v = -INFINITY;
-        }
-        s[jb][e] = v;
-        tmax = fmaxf(tmax, v);
-      }
-    tmax = wave_max32(tmax);
-    const float m_new = fmaxf(m_i, tmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_i - m_use);
-    m_i = m_new;
-    l_i *= alpha;
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[jb][e]);
+    tmax = wave_max32(tmax) * c;
+    const bool bump = tmax > m_i + kLazy;
+    if (__any(bump)) {
+      asm volatile("" ::: "memory");  // keep this a branch (rarely taken), not a select
+      const float m_new = bump ? tmax : m_i;
+      const float alpha = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_new);
+      m_i = m_new;
+      l_i *= alpha;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      o[0][e] *= alpha;
-      o[1][e] *= alpha;
+      for (int e = 0; e < 16; ++e) {
+        o[0][e] *= alpha;
+        o[1][e] *= alpha;
+      }
     }
+    const float m_use = m_i == -INFINITY ? 0.f : m_i;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float p = exp2f(s[jb][e] - m_use);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jb][e], c, -m_use));
         s[jb][e] = p;
         l_i += p;
       }
-    // O^T[dim][query] += V^T[dim][key] . P^T[key][query]
+    // O^T[dim][query] += V^T[dim][key] . P^T[key][query].  The MFMA's k index
+    // 8 * hb + t of a 16-key step u stands for key 16u + 4hb + t (t < 4) or
+    // 16u + 8 + 4hb + (t - 4): the order in which the S^T accumulator holds
+    // them, so P^T needs no data movement and V^T is read to match.
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
@@ -161,18 +222,35 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
         bf16x8_t pf;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pf[e] = static_cast<__bf16>(s[jb][8 * u + e]);
-        const int kb = jb * 32 + 16 * u + 4 * hb;
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
-          const bf16_t* vr = Vt + (db * 32 + l32) * kLdV + kb;
-          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
-          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 8);
-          const u32x4_t vv = {lo[0], lo[1], hi[0], hi[1]};
-          const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, vv);
+          const s16x4_t lo = lds_read_tr(sb + voff[jb][u][db][0]);
+          const s16x4_t hi = lds_read_tr(sb + voff[jb][u][db][1]);
+          const bf16x8_t vf = __builtin_bit_cast(
+              bf16x8_t, (s16x8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
         }
       }
-    __syncthreads();
+  };
+
+#pragma unroll
+  for (int st = 0; st < kNS - 1; ++st)
+    if (st < ntiles) issue(st, st);
+
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + kNS - 2 < ntiles)
+      wait_vmcnt<4 * (kNS - 2)>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (t + kNS - 1 < ntiles) issue(t + kNS - 1, (t + kNS - 1) % kNS);
+    if (!wave_active) continue;
+    const int kt = klo + t * kKey;
+    const char* sb = smem + (t % kNS) * kStage;
+    if (kt + kKey > khi || a.window > 0)
+      tile(std::true_type{}, sb, kt);
+    else
+      tile(std::false_type{}, sb, kt);
   }
 
   const float l_tot = l_i + __shfl_xor(l_i, 32, 64);

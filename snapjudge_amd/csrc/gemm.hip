@@ -265,16 +265,6 @@ struct DTile {
   }
 };
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt immediate");
-  if constexpr (N == 0) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  } else {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-  }
-}
-
 template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs g) {
   using TT = DTile<BM, BN, WGM, WGN, NS, BK>;
@@ -311,10 +301,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs 
     char* base = dsmem + buf * TT::STAGE_BYTES;
 #pragma unroll
     for (int i = 0; i < G; ++i)
-      __builtin_amdgcn_global_load_lds(
-          static_cast<const void*>(src[i] + kt * BK),
-          (__attribute__((address_space(3))) void*)(base + (wave + TT::NW * i) * 1024), 16, 0,
-          0);
+      load_lds16(static_cast<const void*>(src[i] + kt * BK), base + (wave + TT::NW * i) * 1024);
   };
 
   f32x16_t acc[TI][TJ];

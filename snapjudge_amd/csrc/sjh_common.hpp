@@ -19,16 +19,17 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet): the hardware
+// conversion (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<bf16_t>(u >> 16);
+  return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  typedef __attribute__((ext_vector_type(2))) float f2_t;
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf2_t;
+  const bf2_t v = __builtin_convertvector((f2_t){lo, hi}, bf2_t);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // Exact erf GELU, the reference's activation (src/tensor.cpp:96-98).
@@ -63,6 +64,26 @@ template <>
 __device__ __forceinline__ void store_f32<float>(float* p, float v) { *p = v; }
 template <>
 __device__ __forceinline__ void store_f32<bf16_t>(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+
+// Wait until at most N vector-memory operations of this wave are
+// outstanding.  Direct-to-LDS loads complete in issue order, so this is how a
+// kernel knows that the oldest stages of its LDS ring have landed.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt immediate");
+  if constexpr (N == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+  }
+}
+
+// Direct-to-LDS 16-byte load: lane l's 16 bytes from src land at
+// lds_base + 16 * l (lds_base must be the same for the whole wave).
+__device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_base), 16,
+                                   0, 0);
+}
 
 // 64-lane wavefront reductions via DPP-backed shuffles.
 template <typename T>
