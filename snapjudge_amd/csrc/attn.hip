@@ -65,7 +65,8 @@ __device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
 
 __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kNS * kStage];
-  const int b = blockIdx.z, h = blockIdx.y;
+  const int b = a.seq_order ? a.seq_order[blockIdx.z] : static_cast<int>(blockIdx.z);
+  const int h = blockIdx.y;
   const int qlen = a.q_len ? a.q_len[b] : a.uniform_L;
   const int q0 = blockIdx.x * kQ;
   if (q0 >= qlen) return;  // uniform over the workgroup
@@ -276,7 +277,8 @@ constexpr int gKey = 32;  // keys per LDS tile
 
 template <typename T, int DH>
 __global__ __launch_bounds__(gQ) void attn_generic_kernel(AttnArgs a) {
-  const int b = blockIdx.z, h = blockIdx.y;
+  const int b = a.seq_order ? a.seq_order[blockIdx.z] : static_cast<int>(blockIdx.z);
+  const int h = blockIdx.y;
   const int qlen = a.q_len ? a.q_len[b] : a.uniform_L;
   const int q0 = blockIdx.x * gQ;
   if (q0 >= qlen) return;

@@ -247,6 +247,18 @@ void Engine::stage_weights(const sjh_model_desc& d) {
 }
 
 // ------------------------------------------------------------------ batches --
+namespace {
+// Longest sequences first: attention workgroups of a long sequence run
+// longest, so dispatching them first keeps the tail of the launch short.
+void set_order(BatchPlan& p) {
+  p.order.resize(static_cast<size_t>(p.B));
+  for (int b = 0; b < p.B; ++b) p.order[static_cast<size_t>(b)] = b;
+  std::stable_sort(p.order.begin(), p.order.end(), [&](int32_t x, int32_t y) {
+    return p.q_len[static_cast<size_t>(x)] > p.q_len[static_cast<size_t>(y)];
+  });
+}
+}  // namespace
+
 BatchPlan Engine::plan(const int64_t* ids, const int64_t* mask, int B, int L,
                        int32_t* ids_out) const {
   BatchPlan p;
@@ -273,6 +285,7 @@ BatchPlan Engine::plan(const int64_t* ids, const int64_t* mask, int B, int L,
   p.T = static_cast<int>(T);
   p.max_q = 0;
   for (int b = 0; b < B; ++b) p.max_q = std::max(p.max_q, p.q_len[static_cast<size_t>(b)]);
+  set_order(p);
   if (ids_out) {
     for (int b = 0; b < B; ++b) {
       const int rows = p.q_len[static_cast<size_t>(b)];
@@ -296,7 +309,7 @@ void Engine::ensure_workspace(int T, int B) {
   ids_.ensure(t * 4);
   tok_pos_.ensure(t * 4);
   tok_seq_.ensure(t * 4);
-  seqinfo_.ensure(static_cast<size_t>(4) * std::max(nB, 1) * 4);
+  seqinfo_.ensure(static_cast<size_t>(5) * std::max(nB, 1) * 4);
   X_.ensure(t * D * 4);
   Y_.ensure(t * D * as);
   QKV_.ensure(t * 3 * D * as);
@@ -313,14 +326,15 @@ void Engine::ensure_workspace(int T, int B) {
 
 void Engine::upload_batch(const BatchPlan& p, const int32_t* h_ids, const int32_t* h_qtype,
                           hipStream_t st) {
-  // pinned staging: [seq_start | q_len | k_len | qtype] then the token ids
-  const size_t nsi = static_cast<size_t>(4) * p.B;
+  // pinned staging: [seq_start | q_len | k_len | qtype | order] then the token ids
+  const size_t nsi = static_cast<size_t>(5) * p.B;
   h_stage_.ensure((nsi + (h_ids ? p.T : 0)) * 4);
   int32_t* s = h_stage_.as<int32_t>();
   std::memcpy(s, p.seq_start.data(), p.B * 4);
   std::memcpy(s + p.B, p.q_len.data(), p.B * 4);
   std::memcpy(s + 2 * p.B, p.k_len.data(), p.B * 4);
   for (int b = 0; b < p.B; ++b) s[3 * p.B + b] = h_qtype ? h_qtype[b] : 0;
+  std::memcpy(s + 4 * p.B, p.order.data(), p.B * 4);
   hip_check(hipMemcpyAsync(seqinfo_.get(), s, nsi * 4, hipMemcpyHostToDevice, st), "upload seqinfo");
   if (h_ids) {
     std::memcpy(s + nsi, h_ids, static_cast<size_t>(p.T) * 4);
@@ -496,6 +510,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       a.seq_start = seq_start;
       a.q_len = q_len;
       a.k_len = k_len;
+      a.seq_order = si + 4 * p.B;
       a.B = p.B;
       a.H = H_;
       a.Dh = Dh_;
@@ -659,6 +674,7 @@ void Engine::enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st) {
     at.seq_start = si;
     at.q_len = si + p.B;
     at.k_len = si + 2 * p.B;
+    at.seq_order = si + 4 * p.B;
     at.B = p.B;
     at.H = H_;
     at.Dh = Dh_;
@@ -834,6 +850,7 @@ void Engine::encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, f
   p.T = static_cast<int>(T);
   p.L = p.max_q;
   if (p.T == 0) return;
+  set_order(p);
   ensure_workspace(p.T, B);
   // The staging buffer is reused by the next call: make sure the previous
   // upload from it has been consumed before overwriting.

@@ -72,6 +72,7 @@ class PinnedBuf {
 struct BatchPlan {
   int B = 0, L = 0, T = 0, max_q = 0;
   std::vector<int32_t> seq_start, q_len, k_len;
+  std::vector<int32_t> order;  // sequences by decreasing length (attention dispatch order)
 };
 
 class Engine {

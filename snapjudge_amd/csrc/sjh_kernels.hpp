@@ -90,6 +90,7 @@ struct AttnArgs {
   const int* seq_start = nullptr;
   const int* q_len = nullptr;
   const int* k_len = nullptr;
+  const int* seq_order = nullptr;  // optional: workgroup z handles sequence seq_order[z]
   int B = 0, H = 0, Dh = 0;
   int max_q = 0;  // upper bound of q_len over the batch (grid size)
   int uniform_L = 0;
