@@ -8,11 +8,13 @@ random N(0, 0.02) bf16 weights (seed 0), batch 64 x seq 512, row lengths
 ids already resident in HBM (sjh_model_encode_device).
 
 value = valid (non-pad) encoder tokens per second.  Also reported:
-  roofline      -- the dominant kernel (gemm_bf16_dma_kernel, the bf16 MFMA GEMM that
-                   serves QKV+RoPE, Wo+residual, Wi+GEGLU, Wo2+residual):
-                   algorithmic FLOPs per launch / mean launch time, measured
+  roofline      -- the dominant kernel (gemm_bf16_dma_kernel instantiated for
+                   the QKV projection with its RoPE epilogue): algorithmic
+                   FLOPs per launch (2*T*D*3D) / mean launch time, measured
                    with a hipEvent pair around every launch on the model's
-                   stream during the timed steps;
+                   stream during the timed steps; traffic = HBM bytes per
+                   launch from the committed rocprofv3 counter summary;
+  gemm_all_tflops -- the same for all four projection GEMMs together;
   attention_mfma_frac -- the attention kernel's algorithmic FLOPs
                    (4*D*sum(n^2) per layer) over its time, vs bf16 peak;
   p50_latency_b1_ms -- config 2 (batch 1, seq 128, no padding) encoder
@@ -38,6 +40,23 @@ sys.path.insert(0, ROOT)
 METRIC = "encoder tokens/sec at B64×S512 bf16 (1 GPU); attention MFMA % peak; p50 latency at B1"
 PEAK_BF16_TFLOPS = 2500.0
 GEMM_NAMES = ("gemm_qkv_rope", "gemm_wo_resid", "gemm_wi_geglu", "gemm_wo2_resid")
+
+
+# rocprofv3 --pmc summary of the dominant kernel (FETCH_SIZE and WRITE_SIZE
+# passes, each scaled by the same counter on a plain copy of known size)
+QKV_TRAFFIC = os.path.join(ROOT, "profiles", "gemm_qkv_rope_cfg3_traffic.md")
+
+
+def measured_traffic(path):
+    """HBM bytes per launch recorded by the counter runs, or None."""
+    import re
+
+    try:
+        with open(path) as f:
+            m = re.search(r"traffic_bytes_per_launch\s*=\s*([0-9]+)", f.read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
 
 
 def gemm_flops_per_token(D, F, layers):
@@ -147,12 +166,16 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     value = T * args.steps / elapsed
 
+    # the dominant kernel: the QKV projection GEMM with its fused RoPE epilogue
+    # (gemm_bf16_dma_kernel<256,256,4,4,2,64,EPI_ROPE>); algorithmic FLOPs per
+    # launch = 2 * T * D * 3D over the valid tokens
+    qkv_ms, qkv_n = prof["gemm_qkv_rope"]
+    qkv_flops = 2.0 * T * D * 3 * D
+    qkv_avg_s = qkv_ms / 1e3 / qkv_n
+    achieved = qkv_flops / qkv_avg_s / 1e12
+    # all four projection GEMMs together (QKV+RoPE, Wo+res, Wi+GEGLU, Wo2+res)
     gemm_ms = sum(prof[n][0] for n in GEMM_NAMES if n in prof)
-    gemm_launches = sum(prof[n][1] for n in GEMM_NAMES if n in prof)
-    gemm_flops_step = gemm_flops_per_token(D, F, NL) * T
-    flops_per_launch = gemm_flops_step * args.steps / gemm_launches
-    avg_launch_s = gemm_ms / 1e3 / gemm_launches
-    achieved = flops_per_launch / avg_launch_s / 1e12
+    gemm_tflops = gemm_flops_per_token(D, F, NL) * T * args.steps / (gemm_ms / 1e3) / 1e12
     attn_ms, attn_n = prof.get("attention", (0.0, 0))
     attn_flops_step = NL * 4.0 * D * float((lens.astype(np.float64) ** 2).sum())
     attn_tflops = attn_flops_step * args.steps / (attn_ms / 1e3) / 1e12 if attn_ms else 0.0
@@ -192,11 +215,14 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "gemm_bf16_dma_kernel (QKV+RoPE, Wo+res, Wi+GEGLU, Wo2+res)",
-                     "launches_per_step": gemm_launches // args.steps,
-                     "flops_per_launch": flops_per_launch,
-                     "avg_launch_us": round(avg_launch_s * 1e6, 3)},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic(QKV_TRAFFIC),
+                     "kernel": "gemm_bf16_dma_kernel<256, 256, 4, 4, 2, 64, 2, unsigned short> "
+                               "(QKV projection + RoPE epilogue)",
+                     "flops_per_launch": qkv_flops,
+                     "launches_per_step": qkv_n // args.steps,
+                     "avg_launch_us": round(qkv_avg_s * 1e6, 3)},
+        "gemm_all_tflops": round(gemm_tflops, 2),
         "attention_mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
         "attention_tflops": round(attn_tflops, 2),
         "p50_latency_b1_ms": p50,

@@ -66,6 +66,35 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+HOOK_SRC = os.path.join(HERE, "hook", "fast_hip.cpp")
+HOOK_LIB = os.path.join(HERE, "libsnapjudge_fast_hip.so")
+
+
+def build_hook(ref: str | None = None, verbose: bool = False) -> str | None:
+    """Build libsnapjudge_fast_hip.so, the reference's FastSnapjudge class over
+    libsnapjudge_hip.so.  It compiles against the reference's own headers
+    (include/snapjudge/model.hpp for DecisionModel's fields), so it is built
+    only where the reference tree exists; the built library travels with the
+    source tree like libsnapjudge_hip.so.  Returns None without the headers."""
+    ref = ref or os.environ.get("SNAPJUDGE_REF", "/root/reference")
+    inc = os.path.join(ref, "include")
+    if not os.path.exists(os.path.join(inc, "snapjudge", "model.hpp")):
+        return None
+    cxx = shutil.which("g++") or "g++"
+    tmp = HOOK_LIB + ".tmp"
+    cmd = [cxx, "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
+           "-I" + os.path.join(ROOT, "include"), "-I" + inc,
+           "-I" + os.path.join(ref, "third_party"), HOOK_SRC, "-L" + HERE, "-lsnapjudge_hip",
+           "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hook build failed:\n{r.stderr[-6000:]}")
+    os.replace(tmp, HOOK_LIB)
+    if verbose:
+        print(f"built {HOOK_LIB}")
+    return HOOK_LIB
+
+
 if __name__ == "__main__":
     build(verbose=True)
     sys.exit(0)
