@@ -83,6 +83,127 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_rows_kernel(LnArgs a) {
   }
 }
 
+// Vector variant for D % 4 == 0 and D <= 1024: lane l owns the 4-column
+// chunks l, l + 64, ..., so every row moves with 16-byte (fp32) or 8-byte
+// (bf16) accesses.  Same arithmetic as ln_rows_kernel.
+template <typename T>
+struct Vec4;
+template <>
+struct Vec4<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&o)[4]) {
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p);
+    o[0] = v[0], o[1] = v[1], o[2] = v[2], o[3] = v[3];
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&o)[4]) {
+    *reinterpret_cast<f32x4_t*>(p) = f32x4_t{o[0], o[1], o[2], o[3]};
+  }
+};
+template <>
+struct Vec4<bf16_t> {
+  static __device__ __forceinline__ void load(const bf16_t* p, float (&o)[4]) {
+    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(p);
+    o[0] = __uint_as_float(v[0] << 16), o[1] = __uint_as_float(v[0] & 0xffff0000u);
+    o[2] = __uint_as_float(v[1] << 16), o[3] = __uint_as_float(v[1] & 0xffff0000u);
+  }
+  static __device__ __forceinline__ void store(bf16_t* p, const float (&o)[4]) {
+    *reinterpret_cast<u32x2_t*>(p) = u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+  }
+};
+
+template <int NV, typename InT, typename ResT, typename OutT>
+__global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
+  if (r >= a.M) return;
+  const int D = a.D, nch = D >> 2;
+  const int64_t src_row = a.ids ? static_cast<int64_t>(a.ids[r]) : static_cast<int64_t>(r);
+  const InT* in = static_cast<const InT*>(a.in) + src_row * a.ld_in;
+  const ResT* res = a.resid ? static_cast<const ResT*>(a.resid) + static_cast<int64_t>(r) * a.ld_in
+                            : nullptr;
+  float v[NV][4];
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      Vec4<InT>::load(in + 4 * c, v[i]);
+      if (res) {
+        float t[4];
+        Vec4<ResT>::load(res + 4 * c, t);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[i][k] += t[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s += static_cast<double>(v[i][k]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[i][k] = 0.f;
+    }
+  }
+  if (a.xio) {
+    float* xo = a.xio + static_cast<int64_t>(r) * a.ld_in;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < nch) Vec4<float>::store(xo + 4 * (lane + 64 * i), v[i]);
+  }
+  float inv = 1.f, fmean = 0.f;
+  if (a.normalize) {
+    const double mean = wave_sum(s) / static_cast<double>(D);
+    double q = 0.0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < nch)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const double d = static_cast<double>(v[i][k]) - mean;
+          q += d * d;
+        }
+    const double var = wave_sum(q) / static_cast<double>(D);
+    inv = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
+    fmean = static_cast<float>(mean);
+  }
+  float* xo = a.x_out ? a.x_out + static_cast<int64_t>(r) * a.ld_x : nullptr;
+  OutT* yo = a.y_out ? static_cast<OutT*>(a.y_out) + static_cast<int64_t>(r) * a.ld_y : nullptr;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    if (c >= nch) continue;
+    float y[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
+    if (a.normalize) {
+      float w[4] = {1.f, 1.f, 1.f, 1.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.w) Vec4<float>::load(a.w + 4 * c, w);
+      if (a.b) Vec4<float>::load(a.b + 4 * c, b);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        y[k] = (y[k] - fmean) * inv;
+        if (a.w) y[k] = y[k] * w[k];
+        if (a.b) y[k] = y[k] + b[k];
+      }
+    }
+    if (xo) Vec4<float>::store(xo + 4 * c, y);
+    if (yo) Vec4<OutT>::store(yo + 4 * c, y);
+  }
+}
+
+template <int NV, typename InT, typename ResT>
+void ln_vec_dispatch_out(const LnArgs& a, hipStream_t st) {
+  dim3 grid((a.M + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
+  if (a.y_dtype == DT_BF16)
+    ln_vec_kernel<NV, InT, ResT, bf16_t><<<grid, block, 0, st>>>(a);
+  else
+    ln_vec_kernel<NV, InT, ResT, float><<<grid, block, 0, st>>>(a);
+}
+
+template <typename InT, typename ResT>
+void ln_vec_dispatch(const LnArgs& a, hipStream_t st) {
+  switch ((a.D + 255) / 256) {
+    case 1: ln_vec_dispatch_out<1, InT, ResT>(a, st); break;
+    case 2: ln_vec_dispatch_out<2, InT, ResT>(a, st); break;
+    case 3: ln_vec_dispatch_out<3, InT, ResT>(a, st); break;
+    default: ln_vec_dispatch_out<4, InT, ResT>(a, st); break;
+  }
+}
+
 template <int NPL, typename InT, typename ResT>
 void ln_dispatch_out(const LnArgs& a, hipStream_t st) {
   dim3 grid((a.M + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
@@ -182,10 +303,26 @@ void launch_ln(const LnArgs& a, hipStream_t st) {
         "layer_norm: residual write-back needs fp32 rows without a gather");
   require(!a.x_out || a.ld_x >= a.D, "layer_norm: ld_x < D");
   require(!a.y_out || a.ld_y >= a.D, "layer_norm: ld_y < D");
-  if (a.in_dtype == DT_BF16)
+  // vector path: 4-column chunks, every row start 16-byte (fp32) / 8-byte (bf16) aligned
+  auto al = [](const void* p, int dt) {
+    return p == nullptr || (reinterpret_cast<uintptr_t>(p) & (dt == DT_BF16 ? 7u : 15u)) == 0;
+  };
+  const bool vec = a.D % 4 == 0 && a.D <= 1024 && a.ld_in % 4 == 0 && a.ld_x % 4 == 0 &&
+                   a.ld_y % 4 == 0 && al(a.in, a.in_dtype) && al(a.resid, a.resid_dtype) &&
+                   al(a.xio, DT_F32) && al(a.x_out, DT_F32) && al(a.y_out, a.y_dtype) &&
+                   al(a.w, DT_F32) && al(a.b, DT_F32);
+  if (vec) {
+    if (a.in_dtype == DT_BF16)
+      a.resid_dtype == DT_BF16 ? ln_vec_dispatch<bf16_t, bf16_t>(a, st)
+                               : ln_vec_dispatch<bf16_t, float>(a, st);
+    else
+      a.resid_dtype == DT_BF16 ? ln_vec_dispatch<float, bf16_t>(a, st)
+                               : ln_vec_dispatch<float, float>(a, st);
+  } else if (a.in_dtype == DT_BF16) {
     ln_dispatch_res<bf16_t>(a, st);
-  else
+  } else {
     ln_dispatch_res<float>(a, st);
+  }
   check_launch("layer_norm");
 }
 
