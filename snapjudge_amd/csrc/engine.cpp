@@ -316,6 +316,11 @@ void Engine::ensure_workspace(int T, int B) {
   O_.ensure(t * D * as);
   G_.ensure(t * std::max<size_t>(F_, head_layers_ > 0 ? 4 * D : 0) * as);
   if (lora_r_ > 0) Z_.ensure(t * static_cast<size_t>(lora_r_) * 4);
+  {  // up to 16 K splits of a 256-row batch over the widest weight matrix
+    const size_t nw = std::max<size_t>({3 * D, 2 * static_cast<size_t>(F_),
+                                        head_layers_ > 0 ? 4 * D : 0});
+    splitk_.ensure(16 * std::min<size_t>(t, 256) * nw * 4);
+  }
   cap_T_ = nT;
   cap_B_ = nB;
   ++ws_gen_;
@@ -404,7 +409,10 @@ std::vector<std::tuple<const char*, double, int64_t>> Engine::profile_totals() {
   return v;
 }
 
-void Engine::gemm(const char* name, const GemmArgs& g, hipStream_t st) {
+void Engine::gemm(const char* name, const GemmArgs& g0, hipStream_t st) {
+  GemmArgs g = g0;
+  g.partial = splitk_.as<float>();
+  g.partial_cap = static_cast<int64_t>(splitk_.bytes() / 4);
   prof_begin(st);
   launch_gemm(g, st);
   prof_end(name, st);

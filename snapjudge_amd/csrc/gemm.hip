@@ -12,6 +12,8 @@
 // micro-tiles per thread and the same LDS-staged epilogue.  It serves the fp32
 // parity mode and the shapes the MFMA tiling does not cover (tiny models, the
 // scorer's N = 1 projection, LoRA ranks).
+#include <algorithm>
+
 #include "sjh_common.hpp"
 #include "sjh_host.hpp"
 #include "sjh_kernels.hpp"
@@ -265,7 +267,11 @@ struct DTile {
   }
 };
 
-template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
+template <typename OutT>
+__device__ void splitk_output(const GemmArgs& g, int S, int m, int n);
+
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT,
+          bool SPLITK = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs g) {
   using TT = DTile<BM, BN, WGM, WGN, NS, BK>;
   constexpr int TI = TT::TI, TJ = TT::TJ, G = TT::G, RB = TT::RB, CPR = TT::CPR;
@@ -312,10 +318,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nk = g.K / BK;
+  // K steps [k_begin, k_begin + nk): all of K, or one split's slice
+  int k_begin = 0, nk = g.K / BK;
+  if constexpr (SPLITK) {
+    k_begin = blockIdx.y * g.k_chunk;
+    nk = min(g.k_chunk, nk - k_begin);
+  }
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue(s, s);
+    if (s < nk) issue(k_begin + s, s);
 
   // operand rows of this lane; tile bases are multiples of 32, so the
   // swizzle key of row base + l32 is that of l32
@@ -327,7 +338,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs 
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
-    if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
+    if (kt + NS - 1 < nk) issue(k_begin + kt + NS - 1, (kt + NS - 1) % NS);
     const char* sb = dsmem + (kt % NS) * TT::STAGE_BYTES;
     // operand fragments double-buffered across the K steps so the LDS reads
     // of step s + 1 are in flight during the MFMAs of step s
@@ -371,7 +382,27 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs 
     }
   }
 
-  gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tile_n, wm, wn, l32, hb);
+  if constexpr (!SPLITK) {
+    gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tile_n, wm, wn, l32, hb);
+  } else {
+    // Split-K: store this split's partial sums at their W row;
+    // splitk_epilogue_kernel adds the splits in order and applies the
+    // epilogue.  The tile holds every W row its outputs need (GEGLU input and
+    // gate rows, both halves of a RoPE head).
+    float* part = g.partial + static_cast<int64_t>(blockIdx.y) * g.M * g.n_w;
+    const int row_base = m0 + wm * TT::WM + 4 * hb;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int64_t wr = mfma_w_row<BN, TT::WN, EPI>(g, tile_n, wn * TT::WN + j * 32 + l32);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
+          if (m < g.M) part[static_cast<int64_t>(m) * g.n_w + wr] = acc[i][j][e];
+        }
+    }
+  }
 }
 
 template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
@@ -429,6 +460,109 @@ void launch_mfma(const GemmArgs& g, hipStream_t st) {
     launch_mfma_epi<SJH_GEMM_MID>(g, st);
   else
     launch_mfma_epi<64, 128, 2, 2, 2, 64>(g, st);
+}
+
+// ------------------------------------------------------------------ split-K
+// Short batches (M <= 256, e.g. batch-1 latency) have too few output tiles to
+// spread the weight reads over the CUs.  K is cut into splits; each split's
+// partial product goes to g.partial, and splitk_epilogue_kernel adds the
+// splits in order and applies the epilogue (one thread per output).  The
+// kernel boundary between the two is what makes every split's partials
+// visible to the epilogue, whichever XCD wrote them.
+__device__ __forceinline__ float splitk_sum(const GemmArgs& g, int S, int m, int col) {
+  float v = 0.f;
+  for (int sp = 0; sp < S; ++sp) v += g.partial[(static_cast<int64_t>(sp) * g.M + m) * g.n_w + col];
+  return v;
+}
+
+// Output (m, n) of a split-K GEMM from the partial sums of all S splits.
+template <typename OutT>
+__device__ void splitk_output(const GemmArgs& g, int S, int m, int n) {
+  if (g.epi == EPI_RESID) {
+    float v = splitk_sum(g, S, m, n);
+    if (g.bias) v += g.bias[n];
+    g.X[static_cast<int64_t>(m) * g.ldx + n] += v;
+    return;
+  }
+  OutT* out = static_cast<OutT*>(g.out) + static_cast<int64_t>(m) * g.ldo + n;
+  if (g.epi == EPI_GEGLU) {
+    store_f32(out, gelu_erf(splitk_sum(g, S, m, n)) * splitk_sum(g, S, m, g.N + n));
+    return;
+  }
+  float v = splitk_sum(g, S, m, n);
+  if (g.epi == EPI_ROPE) {
+    if (n < 2 * g.rope_dim) {
+      const int half = g.head_dim >> 1, d = n % g.head_dim;
+      const int64_t p = min(max(g.pos[m], 0), g.rope_rows - 1);
+      if (d < half) {
+        v = rope_lo(v, splitk_sum(g, S, m, n + half), g.rope_cos[p * half + d],
+                    g.rope_sin[p * half + d]);
+      } else {
+        v = rope_hi(splitk_sum(g, S, m, n - half), v, g.rope_cos[p * half + d - half],
+                    g.rope_sin[p * half + d - half]);
+      }
+    }
+  } else {
+    if (g.bias) v += g.bias[n];
+    if (g.act == 1)
+      v = gelu_erf(v);
+    else if (g.act == 2)
+      v = fmaxf(v, 0.f);
+  }
+  store_f32(out, v);
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g, int S) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= static_cast<int64_t>(g.M) * g.N) return;
+  const int m = static_cast<int>(idx / g.N);
+  splitk_output<OutT>(g, S, m, static_cast<int>(idx - static_cast<int64_t>(m) * g.N));
+}
+
+// Split-K tile: 128 x 64 with 4 waves of 64 x 32.
+constexpr int kSkBM = 128, kSkBN = 64;
+
+template <int EPI>
+void launch_splitk_epi(const GemmArgs& g, dim3 grid, hipStream_t st) {
+  constexpr int lds = 2 * DTile<kSkBM, kSkBN, 2, 2, 2, 64>::STAGE_BYTES;
+  auto kern = g.out_dtype == DT_BF16 || EPI == EPI_RESID
+                  ? gemm_bf16_dma_kernel<kSkBM, kSkBN, 2, 2, 2, 64, EPI, bf16_t, true>
+                  : gemm_bf16_dma_kernel<kSkBM, kSkBN, 2, 2, 2, 64, EPI, float, true>;
+  kern<<<grid, 256, lds, st>>>(g);
+}
+
+// Returns false (caller takes the regular path) when the workspace is too
+// small or K too short to split.
+bool launch_splitk(const GemmArgs& g0, hipStream_t st) {
+  GemmArgs g = g0;
+  g.n_w = g.epi == EPI_GEGLU ? 2 * g.N : g.N;
+  if (g.epi == EPI_GEGLU && g.N % (kSkBN / 2) != 0) return false;
+  const int tiles_n = g.epi == EPI_GEGLU ? g.N / (kSkBN / 2) : (g.N + kSkBN - 1) / kSkBN;
+  const int tiles = ((g.M + kSkBM - 1) / kSkBM) * tiles_n;
+  const int nk = g.K / kBK;
+  // enough workgroups to cover the CUs, at least two K steps per split
+  int S = std::min(std::max(1, (512 + tiles - 1) / tiles), std::max(1, nk / 2));
+  S = std::min(S, 16);
+  g.k_chunk = (nk + S - 1) / S;
+  S = (nk + g.k_chunk - 1) / g.k_chunk;
+  if (S < 2 || static_cast<int64_t>(S) * g.M * g.n_w > g.partial_cap) return false;
+  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(S));
+  switch (g.epi) {
+    case EPI_STORE: launch_splitk_epi<EPI_STORE>(g, grid, st); break;
+    case EPI_RESID: launch_splitk_epi<EPI_RESID>(g, grid, st); break;
+    case EPI_ROPE: launch_splitk_epi<EPI_ROPE>(g, grid, st); break;
+    default: launch_splitk_epi<EPI_GEGLU>(g, grid, st); break;
+  }
+  check_launch("gemm_splitk");
+  const int64_t outs = static_cast<int64_t>(g.M) * g.N;
+  dim3 eg(static_cast<unsigned>((outs + 255) / 256));
+  if (g.out_dtype == DT_BF16 || g.epi == EPI_RESID)
+    splitk_epilogue_kernel<bf16_t><<<eg, 256, 0, st>>>(g, S);
+  else
+    splitk_epilogue_kernel<float><<<eg, 256, 0, st>>>(g, S);
+  check_launch("gemm_splitk_epilogue");
+  return true;
 }
 
 // ------------------------------------------------------------------ generic
@@ -540,6 +674,7 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
                     (g.epi != EPI_GEGLU || g.N % 64 == 0);
   if (g.epi == EPI_ROPE && !mfma)
     require(gBN % g.head_dim == 0, "gemm: ROPE epilogue needs head_dim dividing 64");
+  if (mfma && g.partial && g.M <= 256 && launch_splitk(g, st)) return;
   if (mfma) {
     launch_mfma(g, st);
     check_launch("gemm_bf16_mfma");

@@ -43,6 +43,14 @@ struct GemmArgs {
   int rope_rows = 0;                // positions are clamped to [0, rope_rows)
   int rope_dim = 0;                 // D: columns [0, 2D) are q and k
   int head_dim = 0;
+  // Optional split-K workspace for short batches (M <= 256): partial sums of
+  // K slices go to partial[split][M][N_w] (fp32) and a second kernel adds them
+  // in split order and applies the epilogue.  Unused when null or too small.
+  float* partial = nullptr;
+  int64_t partial_cap = 0;  // floats
+  // set by the launcher for split-K launches
+  int k_chunk = 0;  // K steps (of the MFMA K depth) per split
+  int n_w = 0;      // rows of W (= N, or 2F for GEGLU)
 };
 void launch_gemm(const GemmArgs& g, hipStream_t st);
 

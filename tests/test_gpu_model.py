@@ -136,7 +136,9 @@ def test_cfg2_full_depth_vs_reference_fixture(cfg2, prec):
 def test_cfg3_shape_sampled_rows_and_batch_invariance(orc):
     # BASELINE config 3's shape (B=64, S=512, n ~ U[64, 512], D=768, F=1152,
     # V=50368) through 2 layers; rows are independent, so sampled rows are
-    # checked against the oracle run on each row alone.
+    # checked against the oracle run on each row alone.  Results do not depend
+    # on padding or on the order of the batch (bit for bit); the GEMM tile
+    # shape follows the token count, so a row alone is held to the tolerance.
     rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg2"], num_hidden_layers=2), seed=21)
     cfg = synth.flat_cfg(rl, enc)
     ids, mask, lens = synth.make_batch(64, 512, 64, 512, cfg["vocab_size"], seed=22)
@@ -150,9 +152,12 @@ def test_cfg3_shape_sampled_rows_and_batch_invariance(orc):
         err = float(np.abs(h[b, :n] - ref).max())
         print(f"row {b} n={n} max|d|={err:.3g}", flush=True)
         assert err <= TOL[BF16]
-        # the same row alone (and with different padding) gives identical bits
+        # the same row alone takes the short-batch GEMM path (split-K): same
+        # tolerance against the oracle; with different padding, identical bits
         alone = m.encode(ids[b:b + 1, :n + 7], mask[b:b + 1, :n + 7])[0, :n]
-        assert np.array_equal(alone, h[b, :n])
+        assert float(np.abs(alone - ref).max()) <= TOL[BF16]
+        alone2 = m.encode(ids[b:b + 1, :n + 3], mask[b:b + 1, :n + 3])[0, :n]
+        assert np.array_equal(alone, alone2)
     # reversing the batch order permutes the outputs and nothing else
     hr = m.encode(ids[::-1].copy(), mask[::-1].copy())
     assert np.array_equal(hr[::-1], h)
