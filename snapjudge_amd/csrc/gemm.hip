@@ -135,6 +135,15 @@ __device__ __forceinline__ int64_t mfma_w_row(const GemmArgs& g, int tile_n, int
   }
 }
 
+// Marks a loaded value as used on every path.  A load whose result some path
+// never reads (rows past M skip their stores) stays pending in the compiler's
+// bookkeeping, which then drains the whole load ring (vmcnt(0)) before the
+// next reuse of its register in the main loop.
+template <typename T>
+__device__ __forceinline__ void consume(const T& v) {
+  asm volatile("" ::"v"(v));
+}
+
 // Epilogue on the accumulators in registers (see the comment above).
 template <int BM, int BN, int WM, int WN, int TI, int TJ, int EPI, typename OutT>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int m0,
@@ -157,52 +166,95 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
         }
       }
   } else if constexpr (EPI == EPI_RESID) {
+    // X += acc (+ bias).  The X reads of a group of RG rows are all issued
+    // before the first add, so a group costs one memory round trip rather
+    // than one per element (rows past M read row M - 1 and store nothing).
+    constexpr int RG = 4;
     const int c0 = tile_n * BN + wn * WN + l32;
     float bv[TJ];
+    int cc[TJ];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) bv[j] = (g.bias && c0 + j * 32 < g.N) ? g.bias[c0 + j * 32] : 0.f;
+    for (int j = 0; j < TJ; ++j) {
+      bv[j] = (g.bias && c0 + j * 32 < g.N) ? g.bias[c0 + j * 32] : 0.f;
+      cc[j] = min(c0 + j * 32, g.N - 1);
+      consume(bv[j]);
+    }
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
-        if (m >= g.M) continue;
-        float* xrow = g.X + static_cast<int64_t>(m) * g.ldx;
+      for (int e0 = 0; e0 < 16; e0 += RG) {
+        float xv[RG][TJ];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-          const int col = c0 + j * 32;
-          if (col < g.N) xrow[col] += acc[i][j][e] + bv[j];
+        for (int e = 0; e < RG; ++e) {
+          const int m = min(row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3), g.M - 1);
+          const float* xrow = g.X + static_cast<int64_t>(m) * g.ldx;
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) xv[e][j] = xrow[cc[j]];
+        }
+#pragma unroll
+        for (int e = 0; e < RG; ++e)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) consume(xv[e][j]);
+#pragma unroll
+        for (int e = 0; e < RG; ++e) {
+          const int m = row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3);
+          if (m >= g.M) continue;
+          float* xrow = g.X + static_cast<int64_t>(m) * g.ldx;
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            if (c0 + j * 32 < g.N) xrow[c0 + j * 32] = xv[e][j] + (acc[i][j][e0 + e] + bv[j]);
         }
       }
   } else if constexpr (EPI == EPI_ROPE) {
     // head_dim 64 (checked by the launcher): block j holds dims [0, 32) of a
     // head when j is even and dims [32, 64) when odd; its partner is j ^ 1.
+    // Positions and table entries of a group of RG rows are fetched together
+    // (two memory round trips per group, not two per row).
     static_assert(TJ % 2 == 0, "RoPE pairs need an even number of column blocks");
+    constexpr int RG = 8;
     OutT* out = static_cast<OutT*>(g.out);
     const int c0 = tile_n * BN + wn * WN;
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
-        if (m >= g.M) continue;
-        OutT* orow = out + static_cast<int64_t>(m) * g.ldo;
-        const int p = min(max(g.pos[m], 0), g.rope_rows - 1);
-        const int64_t tb = static_cast<int64_t>(p) * 32 + l32;
-        const float cs = g.rope_cos[tb], sn = g.rope_sin[tb];
+      for (int e0 = 0; e0 < 16; e0 += RG) {
+        int p[RG];
 #pragma unroll
-        for (int j = 0; j < TJ; j += 2) {
-          const int col = c0 + j * 32 + l32;
-          if (col >= g.N) continue;
-          float x0 = acc[i][j][e], x1 = acc[i][j + 1][e];
-          if (c0 + j * 32 < 2 * g.rope_dim) {
-            const float r0 = rope_lo(x0, x1, cs, sn);
-            const float r1 = rope_hi(x0, x1, cs, sn);
-            x0 = r0;
-            x1 = r1;
+        for (int e = 0; e < RG; ++e) {
+          const int m = min(row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3), g.M - 1);
+          p[e] = g.pos[m];
+        }
+        float cs[RG], sn[RG];
+#pragma unroll
+        for (int e = 0; e < RG; ++e) {
+          const int64_t tb = static_cast<int64_t>(min(max(p[e], 0), g.rope_rows - 1)) * 32 + l32;
+          cs[e] = g.rope_cos[tb];
+          sn[e] = g.rope_sin[tb];
+        }
+#pragma unroll
+        for (int e = 0; e < RG; ++e) {
+          consume(cs[e]);
+          consume(sn[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < RG; ++e) {
+          const int m = row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3);
+          if (m >= g.M) continue;
+          OutT* orow = out + static_cast<int64_t>(m) * g.ldo;
+#pragma unroll
+          for (int j = 0; j < TJ; j += 2) {
+            const int col = c0 + j * 32 + l32;
+            if (col >= g.N) continue;
+            float x0 = acc[i][j][e0 + e], x1 = acc[i][j + 1][e0 + e];
+            if (c0 + j * 32 < 2 * g.rope_dim) {
+              const float r0 = rope_lo(x0, x1, cs[e], sn[e]);
+              const float r1 = rope_hi(x0, x1, cs[e], sn[e]);
+              x0 = r0;
+              x1 = r1;
+            }
+            store_f32(orow + col, x0);
+            if (col + 32 < g.N) store_f32(orow + col + 32, x1);
           }
-          store_f32(orow + col, x0);
-          if (col + 32 < g.N) store_f32(orow + col + 32, x1);
         }
       }
   } else {
@@ -405,6 +457,393 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs 
   }
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---- persistent variant ------------------------------------------------------
+// One workgroup per CU walks a static list of output tiles.  The direct-to-LDS
+// load ring runs across tile boundaries (the first stages of the next tile are
+// in flight while the current tile's epilogue runs), and the MFMAs of the last
+// K step of each stage are issued after the next barrier, so the matrix pipe
+// keeps working while the first operand reads of the new stage are in flight.
+//
+// The MFMA computes the transposed product C^T = W . A^T: W rows are the MFMA
+// rows and A rows its columns.  Lane l then owns output row l % 32 of a 32x32
+// block and, for e = 4q + r, output column 8q + 4(l / 32) + r: four
+// consecutive columns per q, so every epilogue reads and writes 8- or 16-byte
+// vectors.  For RoPE (head_dim 64) the partner of a dim in block j is the same
+// lane and register in block j ^ 1; for GEGLU the input and gate values of an
+// output are the same lane and register in blocks j and j + TJ/2.
+
+__device__ __forceinline__ void store4(bf16_t* p, float a, float b, float c, float d) {
+  *reinterpret_cast<u32x2_t*>(p) = (u32x2_t){pack_bf16x2(a, b), pack_bf16x2(c, d)};
+}
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<f32x4_t*>(p) = (f32x4_t){a, b, c, d};
+}
+
+// Tiles never straddle N (the launcher requires N to be a multiple of the
+// tile's output width), so only rows past M are masked.
+template <int BM, int BN, int WM, int WN, int TI, int TJ, int EPI, typename OutT>
+__device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int m0,
+                                              int tile_n, int wm, int wn, int l32, int hb) {
+  const int row0 = m0 + wm * WM + l32;  // + 32 i
+  if constexpr (EPI == EPI_GEGLU) {
+    OutT* out = static_cast<OutT*>(g.out);
+    const int c0 = tile_n * (BN / 2) + wn * (WN / 2) + 4 * hb;  // + 32 j + 8 q
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      const int m = row0 + i * 32;
+      if (m >= g.M) continue;
+      OutT* orow = out + static_cast<int64_t>(m) * g.ldo + c0;
+#pragma unroll
+      for (int j = 0; j < TJ / 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            v[r] = gelu_erf(acc[i][j][4 * q + r]) * acc[i][j + TJ / 2][4 * q + r];
+          store4(orow + j * 32 + 8 * q, v[0], v[1], v[2], v[3]);
+        }
+    }
+  } else if constexpr (EPI == EPI_RESID) {
+    const int c0 = tile_n * BN + wn * WN + 4 * hb;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      const int m = row0 + i * 32;
+      float* xrow = g.X + static_cast<int64_t>(min(m, g.M - 1)) * g.ldx + c0;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        // the block's four X reads are issued before the first add
+        f32x4_t xv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[q] = *reinterpret_cast<const f32x4_t*>(xrow + j * 32 + 8 * q);
+        if (g.bias) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4_t b = *reinterpret_cast<const f32x4_t*>(g.bias + c0 + j * 32 + 8 * q);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[i][j][4 * q + t] += b[t];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) consume(xv[q]);
+        if (m < g.M) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            f32x4_t r;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) r[t] = xv[q][t] + acc[i][j][4 * q + t];
+            *reinterpret_cast<f32x4_t*>(xrow + j * 32 + 8 * q) = r;
+          }
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_ROPE) {
+    static_assert(TJ % 2 == 0, "RoPE pairs need an even number of column blocks");
+    OutT* out = static_cast<OutT*>(g.out);
+    const int c0 = tile_n * BN + wn * WN + 4 * hb;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      const int m = row0 + i * 32;
+      const int p = min(max(g.pos[min(m, g.M - 1)], 0), g.rope_rows - 1);
+      // dims 8q + 4hb .. +3 at the row's position
+      f32x4_t cs[4], sn[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t tb = static_cast<int64_t>(p) * 32 + 8 * q + 4 * hb;
+        cs[q] = *reinterpret_cast<const f32x4_t*>(g.rope_cos + tb);
+        sn[q] = *reinterpret_cast<const f32x4_t*>(g.rope_sin + tb);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        consume(cs[q]);
+        consume(sn[q]);
+      }
+      if (m >= g.M) continue;
+      OutT* orow = out + static_cast<int64_t>(m) * g.ldo + c0;
+#pragma unroll
+      for (int j = 0; j < TJ; j += 2) {
+        const bool rot = tile_n * BN + wn * WN + j * 32 < 2 * g.rope_dim;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float x0[4], x1[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            x0[t] = acc[i][j][4 * q + t];
+            x1[t] = acc[i][j + 1][4 * q + t];
+            if (rot) {
+              const float r0 = rope_lo(x0[t], x1[t], cs[q][t], sn[q][t]);
+              const float r1 = rope_hi(x0[t], x1[t], cs[q][t], sn[q][t]);
+              x0[t] = r0;
+              x1[t] = r1;
+            }
+          }
+          store4(orow + j * 32 + 8 * q, x0[0], x0[1], x0[2], x0[3]);
+          store4(orow + j * 32 + 32 + 8 * q, x1[0], x1[1], x1[2], x1[3]);
+        }
+      }
+    }
+  } else {
+    OutT* out = static_cast<OutT*>(g.out);
+    const int c0 = tile_n * BN + wn * WN + 4 * hb;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      const int m = row0 + i * 32;
+      if (m >= g.M) continue;
+      OutT* orow = out + static_cast<int64_t>(m) * g.ldo + c0;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4_t b = g.bias ? *reinterpret_cast<const f32x4_t*>(g.bias + c0 + j * 32 + 8 * q)
+                                   : (f32x4_t){0, 0, 0, 0};
+          float v[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            v[t] = acc[i][j][4 * q + t] + b[t];
+            if (g.act == 1)
+              v[t] = gelu_erf(v[t]);
+            else if (g.act == 2)
+              v[t] = fmaxf(v[t], 0.f);
+          }
+          store4(orow + j * 32 + 8 * q, v[0], v[1], v[2], v[3]);
+        }
+    }
+  }
+}
+
+// At most 128 VGPRs (4 waves per SIMD), so that several workgroups of fewer
+// than 16 waves share a CU.
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
+__global__ __launch_bounds__(64 * WGM * WGN, 4) void gemm_bf16_pers_kernel(GemmArgs g) {
+  using TT = DTile<BM, BN, WGM, WGN, NS, BK>;
+  constexpr int TI = TT::TI, TJ = TT::TJ, G = TT::G, RB = TT::RB, CPR = TT::CPR, NW = TT::NW;
+  constexpr int KS = BK / 16;  // MFMA K steps per stage
+  static_assert(KS % 2 == 0, "the deferred step and step 0 use different fragment buffers");
+  // Transposed product (vector epilogue) only where the epilogue just stores:
+  // its 16-byte accesses span 32 rows, which costs more than it saves where
+  // the epilogue also reads (X, RoPE tables).
+  constexpr bool kSwap = EPI == EPI_GEGLU;
+  extern __shared__ __attribute__((aligned(16))) char dsmem[];
+
+  const int tiles_n = EPI == EPI_GEGLU ? g.N / (BN / 2) : g.N / BN;
+  const int tiles = tiles_n * ((g.M + BM - 1) / BM);
+  const int nk = g.K / BK;
+
+  // Static schedule.  Workgroup b runs on XCD b % 8.  The tile list (N
+  // fastest) is cut into 8 contiguous ranges, one per XCD, sized by the
+  // number of workgroups on that XCD, so the tiles sharing an A row panel stay
+  // in one L2; workgroup k of an XCD takes local tiles k, k + c, k + 2c, ...
+  const int nwg = gridDim.x, xcd = blockIdx.x & 7, xk = blockIdx.x >> 3;
+  const int per = nwg >> 3, rem = nwg & 7;
+  const int cx = per + (xcd < rem ? 1 : 0);
+  const int offx = xcd * per + min(xcd, rem);
+  const int lo = static_cast<int>(static_cast<int64_t>(tiles) * offx / nwg);
+  const int hi = static_cast<int>(static_cast<int64_t>(tiles) * (offx + cx) / nwg);
+  const int my_tiles = xk < hi - lo ? (hi - lo - xk + cx - 1) / cx : 0;
+  if (my_tiles == 0) return;
+  const int total = my_tiles * nk;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int l32 = lane & 31, hb = lane >> 5;
+  const bf16_t* A = static_cast<const bf16_t*>(g.A);
+  const bf16_t* W = static_cast<const bf16_t*>(g.W);
+
+  // Load cursor (uniform): tile (ld_m, ld_n) of this workgroup's list and K
+  // step ld_kt.  Each issue recomputes its row addresses from it.
+  const int lrow = lane / CPR, cslot = lane % CPR;
+  int ld_kt = 0, ld_m, ld_n;
+  {
+    const int t0 = lo + xk;
+    ld_m = t0 / tiles_n;
+    ld_n = t0 - ld_m * tiles_n;
+  }
+  const int step_m = cx / tiles_n, step_n = cx - step_m * tiles_n;
+  // Per-lane source rows of the load tile, recomputed only when the cursor
+  // enters a new tile; each stage then adds its K offset.  The LDS target of
+  // each load instruction is wave-uniform and kept in scalar registers.
+  const bf16_t* src[G];
+  auto set_src = [&]() {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int row = TT::RPI * (wave + NW * i) + lrow;
+      const int gchunk = cslot ^ TT::swz(row);
+      if (row < BM)
+        src[i] = A + static_cast<int64_t>(min(ld_m * BM + row, g.M - 1)) * g.lda + gchunk * 8;
+      else
+        src[i] = W + mfma_w_row<BN, TT::WN, EPI>(g, ld_n, row - BM) * g.ldw + gchunk * 8;
+    }
+  };
+  set_src();
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  auto issue_next = [&](int buf) {
+    char* base = dsmem + buf * TT::STAGE_BYTES + wave_s * 1024;
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+      load_lds16(static_cast<const void*>(src[i] + ld_kt * BK), base + NW * i * 1024);
+    if (++ld_kt == nk) {  // next tile of the list: index + cx
+      ld_kt = 0;
+      ld_n += step_n;
+      ld_m += step_m;
+      if (ld_n >= tiles_n) {
+        ld_n -= tiles_n;
+        ++ld_m;
+      }
+      set_src();
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < total) issue_next(s);
+
+  const int xr = TT::swz(l32);
+  const int a_row0 = (wm * TT::WM + l32) * RB, w_row0 = (BM + wn * TT::WN + l32) * RB;
+  bf16x8_t af[2][TI], bw[2][TJ];
+  auto frag = [&](const char* sb, int s, int buf) {
+    const int coff = ((2 * s + hb) ^ xr) * 16;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+      af[buf][i] = *reinterpret_cast<const bf16x8_t*>(sb + a_row0 + i * 32 * RB + coff);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+      bw[buf][j] = *reinterpret_cast<const bf16x8_t*>(sb + w_row0 + j * 32 * RB + coff);
+  };
+  f32x16_t acc[TI][TJ];
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+        acc[i][j] = kSwap ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[buf][j], af[buf][i],
+                                                                     acc[i][j], 0, 0, 0)
+                          : __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[buf][i], bw[buf][j],
+                                                                     acc[i][j], 0, 0, 0);
+  };
+
+  int q = 0;  // global stage counter (ring position)
+  int tm = ld_m, tn = ld_n;  // tile being computed
+  for (int r = 0; r < my_tiles; ++r) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    // fragment buffer 1 starts at zero: the first stage's "deferred" MFMAs add 0
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) af[1][i][t] = static_cast<__bf16>(0.f);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) bw[1][j][t] = static_cast<__bf16>(0.f);
+    for (int kt = 0; kt < nk; ++kt, ++q) {
+      // this wave's loads of stage q have landed once at most the younger
+      // stages' loads are outstanding (vector memory completes in issue order)
+      if (q + NS - 2 < total)
+        wait_vmcnt<G * (NS - 2)>();
+      else
+        wait_vmcnt<0>();
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+      if (q + NS - 1 < total) issue_next((q + NS - 1) % NS);
+      const char* sb = dsmem + (q % NS) * TT::STAGE_BYTES;
+      // operand reads of step 0 go out first; the previous stage's last K
+      // step (deferred past the barrier) covers their latency; then each
+      // step's MFMAs interleave one-for-one with the reads of the next step
+      frag(sb, 0, 0);
+      mma(1);
+#pragma unroll
+      for (int s = 0; s + 1 < KS; ++s) {
+        frag(sb, s + 1, (s + 1) & 1);
+        mma(s & 1);
+      }
+#pragma unroll
+      for (int k = 0; k < TI + TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+      for (int k = 0; k < TI * TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+      for (int s = 0; s + 1 < KS; ++s) {
+#pragma unroll
+        for (int k = 0; k < TI * TJ; ++k) {
+          if (k < TI + TJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+#pragma unroll
+        for (int k = TI * TJ; k < TI + TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+    mma(1);
+    if constexpr (kSwap)
+      pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, tm * BM, tn, wm, wn, l32, hb);
+    else
+      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, tm * BM, tn, wm, wn, l32, hb);
+    tn += step_n;
+    tm += step_m;
+    if (tn >= tiles_n) {
+      tn -= tiles_n;
+      ++tm;
+    }
+  }
+}
+
+int num_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    hip_check(hipGetDevice(&dev), "gemm: hipGetDevice");
+    hip_check(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev),
+              "gemm: CU count");
+    n = v > 0 ? v : 256;
+  }
+  return n;
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
+void launch_pers_kernel(const GemmArgs& g, hipStream_t st) {
+  constexpr int lds = NS * DTile<BM, BN, WGM, WGN, NS, BK>::STAGE_BYTES;
+  auto kern = gemm_bf16_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI, OutT>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+              "gemm: LDS attribute");
+    attr_set = true;
+  }
+  const int tiles_n = EPI == EPI_GEGLU ? g.N / (BN / 2) : g.N / BN;
+  const int64_t tiles = static_cast<int64_t>(tiles_n) * ((g.M + BM - 1) / BM);
+  require(tiles < (int64_t{1} << 30), "gemm: too many tiles");
+  // workgroups resident per CU: bounded by the 160 KB of LDS and by 16 waves
+  // (4 per SIMD at <= 128 VGPRs); several per CU let one workgroup's
+  // barriers and epilogue overlap another's MFMAs
+  constexpr int occ = std::max(1, std::min(163840 / lds, 16 / (WGM * WGN)));
+  const int grid = static_cast<int>(std::min<int64_t>(tiles, int64_t{occ} * num_cus()));
+  kern<<<grid, 64 * WGM * WGN, lds, st>>>(g);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int BK>
+void launch_pers(const GemmArgs& g, hipStream_t st) {
+  const bool bf = g.out_dtype == DT_BF16;
+  switch (g.epi) {
+    case EPI_STORE:
+      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_STORE, bf16_t>(g, st)
+         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_STORE, float>(g, st);
+      break;
+    case EPI_RESID: launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_RESID, float>(g, st); break;
+    case EPI_ROPE:
+      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_ROPE, bf16_t>(g, st)
+         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_ROPE, float>(g, st);
+      break;
+    default:
+      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_GEGLU, bf16_t>(g, st)
+         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_GEGLU, float>(g, st);
+      break;
+  }
+}
+
 template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
 void launch_mfma_kernel(const GemmArgs& g, dim3 grid, hipStream_t st) {
   constexpr int lds = NS * DTile<BM, BN, WGM, WGN, NS, BK>::STAGE_BYTES;
@@ -453,8 +892,21 @@ void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
 // for the throughput shapes; 128x128 with 4 waves for mid-size batches;
 // 64x128 with 4 waves of 32x64 for short ones (batch-1 latency), where more
 // workgroups are needed to spread the weight reads over the CUs.
+#ifndef SJH_GEMM_PERS
+#define SJH_GEMM_PERS 256, 256, 4, 4, 2, 64
+#endif
+constexpr int kPersTile[] = {SJH_GEMM_PERS};
+constexpr int kPersBN = kPersTile[1];
+
 void launch_mfma(const GemmArgs& g, hipStream_t st) {
-  if (g.M >= 4096 && (g.epi != EPI_GEGLU || g.N % 128 == 0))
+  // persistent kernel: N a multiple of the tile's output width (256, GEGLU
+  // 128) and 16-byte aligned rows for its vector epilogue
+  const bool pers = g.N % (g.epi == EPI_GEGLU ? kPersBN / 2 : kPersBN) == 0 && g.ldo % 4 == 0 &&
+                    g.ldx % 4 == 0 && aligned16(g.out) && aligned16(g.X) && aligned16(g.bias) &&
+                    aligned16(g.rope_cos) && aligned16(g.rope_sin);
+  if (g.M >= 4096 && pers)
+    launch_pers<SJH_GEMM_PERS>(g, st);
+  else if (g.M >= 4096 && (g.epi != EPI_GEGLU || g.N % 128 == 0))
     launch_mfma_epi<SJH_GEMM_BIG>(g, st);
   else if (g.M >= 1024)
     launch_mfma_epi<SJH_GEMM_MID>(g, st);
@@ -627,8 +1079,6 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs g) {
   __syncthreads();
   tile_epilogue<gBM, gBN, 256, OutT>(Cs, gLdc, m0, tile_n, g);
 }
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <typename InT>
 void launch_generic(const GemmArgs& g, hipStream_t st) {

@@ -78,6 +78,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   }
 }
 
+// Every LDS read of this wave has returned (lgkmcnt(0)).  A wave that still
+// has operand reads of a ring slot in flight must not pass the barrier after
+// which other waves refill that slot.  Issued through the builtin (not inline
+// asm) so that the compiler's own wait insertion knows that nothing of LGKM
+// is outstanding afterwards.  gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8], vmcnt[5:4] at [15:14]; vmcnt 63 and expcnt 7 wait for nothing.
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+}
+
 // Direct-to-LDS 16-byte load: lane l's 16 bytes from src land at
 // lds_base + 16 * l (lds_base must be the same for the whole wave).
 __device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
