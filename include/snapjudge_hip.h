@@ -43,8 +43,14 @@ enum { SJH_F32 = 0, SJH_BF16 = 1 }; /* element types */
  *  SJH_PREC_FP32: fp32 weights and activations, fp32 accumulation
  *                 (parity mode: hidden states within 1e-4 of the reference).
  *  SJH_PREC_BF16: bf16 weights and activations, fp32 accumulation, fp32
- *                 residual stream and LayerNorm statistics (within 2e-2). */
-enum { SJH_PREC_FP32 = 0, SJH_PREC_BF16 = 1 };
+ *                 residual stream and LayerNorm statistics (within 2e-2).
+ *  SJH_PREC_FP8W: as SJH_PREC_BF16, but the four encoder projections of every
+ *                 layer (Wqkv, Wo, Wi, Wo2) are stored as OCP fp8 e4m3 with
+ *                 one fp32 scale per output row (sjh_quantize_fp8); the
+ *                 forward equals the reference forward on the dequantized
+ *                 weights within the bf16 tolerance.  No counterpart in the
+ *                 reference, whose loader rejects fp8 (src/safetensors.cpp:132). */
+enum { SJH_PREC_FP32 = 0, SJH_PREC_BF16 = 1, SJH_PREC_FP8W = 2 };
 
 /* One encoder layer: the reference's LayerWeights (include/snapjudge/model.hpp:37-44),
  * fp32 host arrays, row-major, PyTorch Linear layout [out, in]. */
@@ -151,6 +157,20 @@ int sjh_model_profile_read(sjh_model* m, int32_t max_entries, const char** names
  * act 0 none, 1 erf-GELU, 2 ReLU.  dtype applies to A, W and C; bias fp32 or NULL. */
 int sjh_gemm(const void* A, const void* W, const float* bias, void* C, int32_t M, int32_t N,
              int32_t K, int32_t act, int32_t dtype, sjh_stream_t stream);
+
+/* Host-side quantizer of SJH_PREC_FP8W (no GPU needed): for each row r of the
+ * row-major [rows, cols] fp32 matrix w, scale[r] = max|w[r,:]| / 448 (1 for an
+ * all-zero row) and q[r,c] = e4m3(w[r,c] / scale[r]), OCP e4m3fn rounded to
+ * nearest even, saturating at 448.  Row r stands for e4m3_decode(q[r,:]) *
+ * scale[r].  No counterpart in the reference (fp8 is not loadable there). */
+int sjh_quantize_fp8(const float* w, int64_t rows, int64_t cols, uint8_t* q, float* scale);
+
+/* sj_gemm with fp8 weights: C[M,N] (bf16) = act(A[M,K] (bf16) . Wdq[N,K]^T (+ bias))
+ * where Wdq[n,:] = e4m3_decode(Wq[n,:]) * w_scale[n].  K % 64 == 0, N % 4 == 0,
+ * 16-byte aligned rows.  The GEMM of SJH_PREC_FP8W models; no counterpart in
+ * the reference. */
+int sjh_gemm_fp8w(const void* A, const uint8_t* Wq, const float* w_scale, const float* bias,
+                  void* C, int32_t M, int32_t N, int32_t K, int32_t act, sjh_stream_t stream);
 
 /* sj_gemm_geglu (cuda/kernels.cu:168-174): C[M,F] = gelu(A.Wi[:F]^T) * (A.Wi[F:]^T),
  * Wi [2F, K]. */

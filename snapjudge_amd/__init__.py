@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsnapjudge_hip.so")
 
 SJH_F32, SJH_BF16 = 0, 1
-SJH_PREC_FP32, SJH_PREC_BF16 = 0, 1
+SJH_PREC_FP32, SJH_PREC_BF16, SJH_PREC_FP8W = 0, 1, 2
 
 _fp = C.POINTER(C.c_float)
 _i64p = C.POINTER(C.c_int64)
@@ -77,6 +77,9 @@ _SIGS = {
                                          C.POINTER(C.c_double), _i64p, _i32p]),
     "sjh_gemm": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                            C.c_int32, C.c_int32, C.c_int32, C.c_void_p]),
+    "sjh_quantize_fp8": (C.c_int, [_fp, C.c_int64, C.c_int64, _u8p, _fp]),
+    "sjh_gemm_fp8w": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p]),
     "sjh_gemm_geglu": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                  C.c_int32, C.c_int32, C.c_void_p]),
     "sjh_gemm_residual": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
@@ -130,6 +133,43 @@ def _ptr(a: np.ndarray | None):
         return None
     assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], "weights must be C-contiguous fp32"
     return a.ctypes.data_as(_fp)
+
+
+def quantize_fp8(w: np.ndarray):
+    """Per-row e4m3 codes and fp32 scales of a 2-D fp32 matrix (sjh_quantize_fp8)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), dtype=np.uint8)
+    sc = np.empty(rows, dtype=np.float32)
+    check(lib().sjh_quantize_fp8(w.ctypes.data_as(_fp), rows, cols, q.ctypes.data_as(_u8p),
+                                 sc.ctypes.data_as(_fp)))
+    return q, sc
+
+
+FP8_PROJECTIONS = ("attn.Wqkv.weight", "attn.Wo.weight", "mlp.Wi.weight", "mlp.Wo.weight")
+
+
+def fp8_dequantized(weights: "dict") -> "dict":
+    """The weights an SJH_PREC_FP8W model computes with: every encoder
+    projection replaced by decode(q) * scale of its sjh_quantize_fp8 codes (the
+    reference forward on this dict is the fp8 model's oracle)."""
+    table = fp8_e4m3_table()
+    out = dict(weights)
+    for k, v in weights.items():
+        if k.startswith("encoder.layers.") and k.split(".", 3)[-1] in FP8_PROJECTIONS:
+            q, sc = quantize_fp8(v)
+            out[k] = (table[q] * sc[:, None]).astype(np.float32)
+    return out
+
+
+def fp8_e4m3_table() -> np.ndarray:
+    """Value of each OCP e4m3fn code (bias 7, 3 mantissa bits, S.1111.111 NaN)."""
+    c = np.arange(256)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e, m = (c >> 3) & 15, c & 7
+    v = np.where(e == 0, m * 2.0 ** -9, (1 + m / 8) * 2.0 ** (e - 7.0))
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return (sign * v).astype(np.float32)
 
 
 class Model:

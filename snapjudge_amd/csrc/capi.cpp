@@ -184,6 +184,39 @@ int sjh_gemm(const void* A, const void* W, const float* bias, void* C, int32_t M
   });
 }
 
+int sjh_quantize_fp8(const float* w, int64_t rows, int64_t cols, uint8_t* q, float* scale) {
+  return guarded([&] {
+    if (rows < 0 || cols < 0) sjh::fail("quantize_fp8: negative shape");
+    if (rows > 0 && cols > 0 && (!w || !q || !scale)) sjh::fail("quantize_fp8: null argument");
+    sjh::quantize_fp8_rows(w, static_cast<size_t>(rows), static_cast<size_t>(cols), q, scale);
+  });
+}
+
+int sjh_gemm_fp8w(const void* A, const uint8_t* Wq, const float* w_scale, const float* bias,
+                  void* C, int32_t M, int32_t N, int32_t K, int32_t act, sjh_stream_t stream) {
+  return guarded([&] {
+    if (act < 0 || act > 2) sjh::fail("act must be 0, 1 or 2");
+    sjh::GemmArgs g;
+    g.A = A;
+    g.lda = K;
+    g.W = Wq;
+    g.ldw = K;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.in_dtype = SJH_BF16;
+    g.w_dtype = sjh::DT_FP8;
+    g.w_scale = w_scale;
+    g.epi = sjh::EPI_STORE;
+    g.out = C;
+    g.ldo = N;
+    g.out_dtype = SJH_BF16;
+    g.bias = bias;
+    g.act = act;
+    sjh::launch_gemm(g, as_stream(stream));
+  });
+}
+
 int sjh_gemm_geglu(const void* A, const void* Wi, void* C, int32_t M, int32_t F, int32_t K,
                    int32_t dtype, sjh_stream_t stream) {
   return guarded([&] {

@@ -57,6 +57,46 @@ void PinnedBuf::ensure(size_t bytes) {
   bytes_ = bytes;
 }
 
+// OCP e4m3fn (1 sign, 4 exponent bits with bias 7, 3 mantissa bits; no
+// infinity, S.1111.111 is NaN, largest finite 448), round to nearest with
+// ties to even; magnitudes of 448 and above (and infinities) saturate to 448.
+uint8_t fp8_e4m3_rne(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  const uint8_t sign = static_cast<uint8_t>((u >> 24) & 0x80u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7f;   // NaN
+  if (a >= 0x43e00000u) return sign | 0x7e;  // >= 448
+  if (a < 0x3c800000u) {                     // below 2^-6: subnormal steps of 2^-9
+    float f;
+    std::memcpy(&f, &a, 4);
+    const float m = std::nearbyint(f * 512.0f);  // exact scaling; default mode rounds to even
+    return sign | static_cast<uint8_t>(m);       // m == 8 is the smallest normal, code 0x08
+  }
+  // normal: round the 23-bit mantissa to 3 bits (ties to even); a carry
+  // moves into the exponent
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  const uint32_t code = ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+  return sign | static_cast<uint8_t>(code > 0x7eu ? 0x7eu : code);
+}
+
+// Per-row symmetric quantization: scale[r] = max |w[r, :]| / 448 (1 for an
+// all-zero row), q[r, c] = e4m3(w[r, c] / scale[r]).  Row r then stands for
+// decode(q[r, :]) * scale[r].
+void quantize_fp8_rows(const float* w, size_t rows, size_t cols, uint8_t* q, float* scale) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float* row = w + r * cols;
+    float amax = 0.f;
+    for (size_t c = 0; c < cols; ++c) {
+      const float v = std::fabs(row[c]);
+      if (v > amax) amax = v;  // NaN compares false
+    }
+    const float sc = (amax > 0.f && std::isfinite(amax)) ? amax / 448.0f : 1.0f;
+    scale[r] = sc;
+    for (size_t c = 0; c < cols; ++c) q[r * cols + c] = fp8_e4m3_rne(row[c] / sc);
+  }
+}
+
 namespace {
 
 uint16_t bf16_rne(float f) {
@@ -83,6 +123,24 @@ DevBuf upload_bf16(const float* src, size_t n, const char* what) {
   b.alloc(n * sizeof(uint16_t));
   hip_check(hipMemcpy(b.get(), tmp.data(), n * sizeof(uint16_t), hipMemcpyHostToDevice), what);
   return b;
+}
+
+// Row-wise fp8 weights: rows x cols codes plus one fp32 scale per row.
+struct Fp8Dev {
+  DevBuf q, scale;
+};
+
+Fp8Dev upload_fp8(const float* src, size_t rows, size_t cols, const char* what) {
+  if (!src) fail(std::string("model descriptor: missing ") + what);
+  std::vector<uint8_t> q(rows * cols);
+  std::vector<float> sc(rows);
+  quantize_fp8_rows(src, rows, cols, q.data(), sc.data());
+  Fp8Dev d;
+  d.q.alloc(q.size());
+  d.scale.alloc(rows * sizeof(float));
+  hip_check(hipMemcpy(d.q.get(), q.data(), q.size(), hipMemcpyHostToDevice), what);
+  hip_check(hipMemcpy(d.scale.get(), sc.data(), rows * sizeof(float), hipMemcpyHostToDevice), what);
+  return d;
 }
 
 DevBuf upload_opt_f32(const float* src, size_t n, const char* what) {
@@ -125,9 +183,12 @@ Engine::Engine(const sjh_model_desc& d, const sjh_options& o) {
   if (std::string(prop.gcnArchName).find("gfx950") == std::string::npos)
     fail(std::string("device is ") + prop.gcnArchName + "; this library is built for gfx950");
 
-  require(o.precision == SJH_PREC_FP32 || o.precision == SJH_PREC_BF16, "unknown precision");
+  require(o.precision == SJH_PREC_FP32 || o.precision == SJH_PREC_BF16 ||
+              o.precision == SJH_PREC_FP8W,
+          "unknown precision");
   prec_ = o.precision;
-  act_dt_ = prec_ == SJH_PREC_BF16 ? DT_BF16 : DT_F32;
+  act_dt_ = prec_ == SJH_PREC_FP32 ? DT_F32 : DT_BF16;
+  w8_ = prec_ == SJH_PREC_FP8W;
   use_graphs_ = o.use_graphs != 0;
   pad_rows_ = o.pad_rows != 0;
 
@@ -145,6 +206,8 @@ Engine::Engine(const sjh_model_desc& d, const sjh_options& o) {
   Dh_ = D_ / H_;
   require(Dh_ % 2 == 0, "head_dim must be even");
   require(F_ > 0 && V_ > 0 && nlayers_ > 0 && max_pos_ > 0, "bad model dimensions");
+  require(!w8_ || (D_ % 64 == 0 && F_ % 64 == 0),
+          "fp8 weights need hidden_size and intermediate_size multiples of 64");
   require(n_act_ > 0 && head_layers_ >= 0 && lora_r_ >= 0, "bad head dimensions");
   require(d.layers != nullptr, "model descriptor: missing layers");
   require(head_layers_ == 0 || d.head != nullptr, "model descriptor: missing head layers");
@@ -202,11 +265,20 @@ void Engine::stage_weights(const sjh_model_desc& d) {
     LayerDev& L = layers_[static_cast<size_t>(i)];
     L.has_attn_norm = s0.attn_norm != nullptr;
     if (L.has_attn_norm) L.attn_norm = upload_f32(s0.attn_norm, D, "attn_norm");
-    L.wqkv = upload_w(s0.wqkv, 3 * D * D, "wqkv");
-    L.wo = upload_w(s0.wo, D * D, "wo");
     L.mlp_norm = upload_f32(s0.mlp_norm, D, "mlp_norm");
-    L.wi = upload_w(s0.wi, 2 * F * D, "wi");
-    L.wo2 = upload_w(s0.wo2, D * F, "wo2");
+    if (w8_) {  // the four projections as per-row fp8 (src/model.cpp:96-128 shapes)
+      Fp8Dev a = upload_fp8(s0.wqkv, 3 * D, D, "wqkv"), b = upload_fp8(s0.wo, D, D, "wo"),
+             c2 = upload_fp8(s0.wi, 2 * F, D, "wi"), e = upload_fp8(s0.wo2, D, F, "wo2");
+      L.wqkv = std::move(a.q), L.wqkv_s = std::move(a.scale);
+      L.wo = std::move(b.q), L.wo_s = std::move(b.scale);
+      L.wi = std::move(c2.q), L.wi_s = std::move(c2.scale);
+      L.wo2 = std::move(e.q), L.wo2_s = std::move(e.scale);
+    } else {
+      L.wqkv = upload_w(s0.wqkv, 3 * D * D, "wqkv");
+      L.wo = upload_w(s0.wo, D * D, "wo");
+      L.wi = upload_w(s0.wi, 2 * F * D, "wi");
+      L.wo2 = upload_w(s0.wo2, D * F, "wo2");
+    }
     require(s0.window >= 0, "negative attention window");
     L.window = s0.window;
     L.sliding = s0.sliding;
@@ -489,6 +561,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.A = Y;
       g.lda = D;
       g.W = ly.wqkv.get();
+      if (w8_) g.w_dtype = DT_FP8, g.w_scale = ly.wqkv_s.as<float>();
       g.ldw = D;
       g.M = T;
       g.N = 3 * D;
@@ -532,6 +605,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.A = O;
       g.lda = D;
       g.W = ly.wo.get();
+      if (w8_) g.w_dtype = DT_FP8, g.w_scale = ly.wo_s.as<float>();
       g.ldw = D;
       g.M = T;
       g.N = D;
@@ -561,6 +635,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.A = Y;
       g.lda = D;
       g.W = ly.wi.get();
+      if (w8_) g.w_dtype = DT_FP8, g.w_scale = ly.wi_s.as<float>();
       g.ldw = D;
       g.M = T;
       g.N = F;
@@ -577,6 +652,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.A = G;
       g.lda = F;
       g.W = ly.wo2.get();
+      if (w8_) g.w_dtype = DT_FP8, g.w_scale = ly.wo2_s.as<float>();
       g.ldw = F;
       g.M = T;
       g.N = D;

@@ -30,6 +30,10 @@
 
 namespace sjh {
 
+// Host-side fp8 quantizer of the SJH_PREC_FP8W mode (engine.cpp).
+uint8_t fp8_e4m3_rne(float x);
+void quantize_fp8_rows(const float* w, size_t rows, size_t cols, uint8_t* q, float* scale);
+
 class DevBuf {
  public:
   DevBuf() = default;
@@ -98,6 +102,7 @@ class Engine {
  private:
   struct LayerDev {
     DevBuf attn_norm, wqkv, wo, mlp_norm, wi, wo2;
+    DevBuf wqkv_s, wo_s, wi_s, wo2_s;  // per-row scales of fp8 projections
     bool has_attn_norm = false;
     int window = 0, sliding = 0;
   };
@@ -133,6 +138,7 @@ class Engine {
   int dev_ = 0;
   int prec_ = SJH_PREC_BF16;
   int act_dt_ = DT_BF16;  // activation / GEMM operand type
+  bool w8_ = false;       // encoder projections stored as fp8 e4m3 + per-row scales
   int D_ = 0, H_ = 0, Dh_ = 0, F_ = 0, V_ = 0, nlayers_ = 0, max_pos_ = 0;
   int n_act_ = 0, head_layers_ = 0, lora_r_ = 0, max_len_ = 0;
   float eps_ = 1e-5f;

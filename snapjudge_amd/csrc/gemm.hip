@@ -481,8 +481,8 @@ __device__ __forceinline__ void store4(float* p, float a, float b, float c, floa
   *reinterpret_cast<f32x4_t*>(p) = (f32x4_t){a, b, c, d};
 }
 
-// Tiles never straddle N (the launcher requires N to be a multiple of the
-// tile's output width), so only rows past M are masked.
+// Rows past M and (GEGLU, whose last column tile may be partial) column
+// chunks past N are masked; N % 4 == 0.
 template <int BM, int BN, int WM, int WN, int TI, int TJ, int EPI, typename OutT>
 __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int m0,
                                               int tile_n, int wm, int wn, int l32, int hb) {
@@ -499,6 +499,7 @@ __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)
       for (int j = 0; j < TJ / 2; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+          if (c0 + j * 32 + 8 * q >= g.N) continue;  // N % 4 == 0: a chunk is all in or out
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
@@ -613,12 +614,58 @@ __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)
   }
 }
 
-// At most 128 VGPRs (4 waves per SIMD), so that several workgroups of fewer
-// than 16 waves share a CU.
-template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
-__global__ __launch_bounds__(64 * WGM * WGN, 4) void gemm_bf16_pers_kernel(GemmArgs g) {
-  using TT = DTile<BM, BN, WGM, WGN, NS, BK>;
-  constexpr int TI = TT::TI, TJ = TT::TJ, G = TT::G, RB = TT::RB, CPR = TT::CPR, NW = TT::NW;
+// Ring geometry of the persistent kernel.  A rows are bf16; W rows are bf16,
+// or fp8 (W8: one byte per element, half the bytes per stage).  Each load
+// instruction fills 1 KB of LDS (64 lanes x 16 bytes): groups [0, GA) are A
+// rows, groups [GA, GA + GW) W rows, and group g lands at byte 1024 g of the
+// stage.  16-byte chunks are XOR-swizzled per row so that the operand reads
+// are free of bank conflicts (16 lanes per cycle over 64 four-byte banks).
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8>
+struct PTile {
+  static constexpr int NW = WGM * WGN;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
+  static constexpr int TI = WM / 32, TJ = WN / 32;
+  static constexpr int RBA = BK * 2, RBW = W8 ? BK : BK * 2;  // bytes per row
+  static constexpr int CPRA = RBA / 16, CPRW = RBW / 16;      // 16-byte chunks per row
+  static constexpr int RPIA = 1024 / RBA, RPIW = 1024 / RBW;  // rows per load instruction
+  static constexpr int GA = BM / RPIA, GW = BN / RPIW;
+  static constexpr int G = (GA + GW) / NW;  // load instructions per wave per stage
+  static constexpr int W_OFF = BM * RBA;
+  static constexpr int STAGE_BYTES = W_OFF + BN * RBW;
+  static_assert(BK == 32 || BK == 64, "K step is 32 or 64");
+  static_assert(!W8 || BK == 64, "fp8 weights use 64-deep K steps");
+  static_assert(G * NW == GA + GW && BM % RPIA == 0 && BN % RPIW == 0,
+                "row groups must split evenly over waves");
+  static_assert(TI >= 1 && TJ >= 1, "tile too small");
+  static_assert(NS >= 2 && NS * STAGE_BYTES <= 160 * 1024, "LDS ring does not fit");
+  static_assert(G * (NS - 2) <= 63, "vmcnt range");
+  // 128-byte rows: 16 consecutive rows at one logical chunk hit 16 distinct
+  // 16-byte bank groups with key (r >> 1) & 7; 64-byte rows need (r >> 2) & 3
+  static __device__ __forceinline__ int swz(int row_bytes, int r) {
+    return row_bytes == 128 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+  }
+};
+
+// Workgroups resident per CU: bounded by the 160 KB of LDS and by 16 waves
+// (4 per SIMD at <= 128 VGPRs).  Several per CU let one workgroup's barriers
+// and epilogue overlap another's MFMAs; the register budget follows from the
+// waves that then share a SIMD.
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8>
+constexpr int pers_occupancy() {
+  return std::max(1, std::min(163840 / (NS * PTile<BM, BN, WGM, WGN, NS, BK, W8>::STAGE_BYTES),
+                              16 / (WGM * WGN)));
+}
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8>
+constexpr int pers_waves_per_simd() {
+  return std::max(1, std::min(4, pers_occupancy<BM, BN, WGM, WGN, NS, BK, W8>() * WGM * WGN / 4));
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8, int EPI, typename OutT>
+__global__ __launch_bounds__(64 * WGM * WGN, (pers_waves_per_simd<BM, BN, WGM, WGN, NS, BK, W8>()))
+void gemm_bf16_pers_kernel(GemmArgs g) {
+  using TT = PTile<BM, BN, WGM, WGN, NS, BK, W8>;
+  constexpr int TI = TT::TI, TJ = TT::TJ, G = TT::G, NW = TT::NW;
+  constexpr int RBA = TT::RBA, RBW = TT::RBW;
   constexpr int KS = BK / 16;  // MFMA K steps per stage
   static_assert(KS % 2 == 0, "the deferred step and step 0 use different fragment buffers");
   // Transposed product (vector epilogue) only where the epilogue just stores:
@@ -627,7 +674,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 4) void gemm_bf16_pers_kernel(GemmA
   constexpr bool kSwap = EPI == EPI_GEGLU;
   extern __shared__ __attribute__((aligned(16))) char dsmem[];
 
-  const int tiles_n = EPI == EPI_GEGLU ? g.N / (BN / 2) : g.N / BN;
+  const int tiles_n = EPI == EPI_GEGLU ? (g.N + BN / 2 - 1) / (BN / 2) : (g.N + BN - 1) / BN;
   const int tiles = tiles_n * ((g.M + BM - 1) / BM);
   const int nk = g.K / BK;
 
@@ -648,12 +695,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 4) void gemm_bf16_pers_kernel(GemmA
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
   const int l32 = lane & 31, hb = lane >> 5;
-  const bf16_t* A = static_cast<const bf16_t*>(g.A);
-  const bf16_t* W = static_cast<const bf16_t*>(g.W);
+  const char* A = static_cast<const char*>(g.A);
+  const char* W = static_cast<const char*>(g.W);
 
   // Load cursor (uniform): tile (ld_m, ld_n) of this workgroup's list and K
-  // step ld_kt.  Each issue recomputes its row addresses from it.
-  const int lrow = lane / CPR, cslot = lane % CPR;
+  // step ld_kt.
   int ld_kt = 0, ld_m, ld_n;
   {
     const int t0 = lo + xk;
@@ -661,28 +707,40 @@ __global__ __launch_bounds__(64 * WGM * WGN, 4) void gemm_bf16_pers_kernel(GemmA
     ld_n = t0 - ld_m * tiles_n;
   }
   const int step_m = cx / tiles_n, step_n = cx - step_m * tiles_n;
+  // compute cursor: the tile whose stages are consumed; taken before the
+  // prologue, whose loads move the load cursor past the first tile when a
+  // tile has fewer K steps than the ring has stages in flight
+  int tm = ld_m, tn = ld_n;
   // Per-lane source rows of the load tile, recomputed only when the cursor
   // enters a new tile; each stage then adds its K offset.  The LDS target of
   // each load instruction is wave-uniform and kept in scalar registers.
-  const bf16_t* src[G];
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const char* src[G];
+  int kbytes[G];  // bytes per K step of the group's operand
+#pragma unroll
+  for (int i = 0; i < G; ++i) kbytes[i] = wave_s + NW * i < TT::GA ? BK * 2 : RBW;
   auto set_src = [&]() {
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-      const int row = TT::RPI * (wave + NW * i) + lrow;
-      const int gchunk = cslot ^ TT::swz(row);
-      if (row < BM)
-        src[i] = A + static_cast<int64_t>(min(ld_m * BM + row, g.M - 1)) * g.lda + gchunk * 8;
-      else
-        src[i] = W + mfma_w_row<BN, TT::WN, EPI>(g, ld_n, row - BM) * g.ldw + gchunk * 8;
+      const int gi = wave + NW * i;
+      if (gi < TT::GA) {
+        const int row = TT::RPIA * gi + lane / TT::CPRA;
+        const int chunk = (lane % TT::CPRA) ^ TT::swz(RBA, row);
+        src[i] = A + static_cast<int64_t>(min(ld_m * BM + row, g.M - 1)) * g.lda * 2 + chunk * 16;
+      } else {
+        const int row = TT::RPIW * (gi - TT::GA) + lane / TT::CPRW;
+        const int chunk = (lane % TT::CPRW) ^ TT::swz(RBW, row);
+        src[i] = W + mfma_w_row<BN, TT::WN, EPI>(g, ld_n, row) * g.ldw * (W8 ? 1 : 2) +
+                 chunk * 16;
+      }
     }
   };
   set_src();
-  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto issue_next = [&](int buf) {
     char* base = dsmem + buf * TT::STAGE_BYTES + wave_s * 1024;
 #pragma unroll
     for (int i = 0; i < G; ++i)
-      load_lds16(static_cast<const void*>(src[i] + ld_kt * BK), base + NW * i * 1024);
+      load_lds16(static_cast<const void*>(src[i] + ld_kt * kbytes[i]), base + NW * i * 1024);
     if (++ld_kt == nk) {  // next tile of the list: index + cx
       ld_kt = 0;
       ld_n += step_n;
@@ -698,32 +756,56 @@ __global__ __launch_bounds__(64 * WGM * WGN, 4) void gemm_bf16_pers_kernel(GemmA
   for (int s = 0; s < NS - 1; ++s)
     if (s < total) issue_next(s);
 
-  const int xr = TT::swz(l32);
-  const int a_row0 = (wm * TT::WM + l32) * RB, w_row0 = (BM + wn * TT::WN + l32) * RB;
-  bf16x8_t af[2][TI], bw[2][TJ];
+  // Operand reads.  bf16 W: step s reads chunk 2s + hb of the A and W rows.
+  // fp8 W: one 16-byte read of W chunk 2p + hb holds 16 K values for the
+  // step pair (2p, 2p + 1), so the K order is permuted the same way on the A
+  // side: step 2p + t reads A chunk 4p + 2hb + t.  The sum over K is the same
+  // either way.
+  const int xa = TT::swz(RBA, l32), xw = TT::swz(RBW, l32);
+  const int a_row0 = (wm * TT::WM + l32) * RBA, w_row0 = TT::W_OFF + (wn * TT::WN + l32) * RBW;
+  bf16x8_t af[2][TI];
+  bf16x8_t bw[W8 ? 1 : 2][TJ];
+  u32x4_t wraw[W8 ? 2 : 1][TJ];  // fp8 codes of a step pair, by pair parity
   auto frag = [&](const char* sb, int s, int buf) {
-    const int coff = ((2 * s + hb) ^ xr) * 16;
+    const int ca = W8 ? 4 * (s >> 1) + 2 * hb + (s & 1) : 2 * s + hb;
 #pragma unroll
     for (int i = 0; i < TI; ++i)
-      af[buf][i] = *reinterpret_cast<const bf16x8_t*>(sb + a_row0 + i * 32 * RB + coff);
-#pragma unroll
-    for (int j = 0; j < TJ; ++j)
-      bw[buf][j] = *reinterpret_cast<const bf16x8_t*>(sb + w_row0 + j * 32 * RB + coff);
-  };
-  f32x16_t acc[TI][TJ];
-  auto mma = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
+      af[buf][i] = *reinterpret_cast<const bf16x8_t*>(sb + a_row0 + i * 32 * RBA + ((ca ^ xa) << 4));
+    if constexpr (!W8) {
 #pragma unroll
       for (int j = 0; j < TJ; ++j)
-        acc[i][j] = kSwap ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[buf][j], af[buf][i],
-                                                                     acc[i][j], 0, 0, 0)
-                          : __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[buf][i], bw[buf][j],
-                                                                     acc[i][j], 0, 0, 0);
+        bw[buf][j] = *reinterpret_cast<const bf16x8_t*>(sb + w_row0 + j * 32 * RBW +
+                                                        (((2 * s + hb) ^ xw) << 4));
+    } else if ((s & 1) == 0) {
+      const int cw = (s & 2) + hb;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+        wraw[(s >> 1) & 1][j] =
+            *reinterpret_cast<const u32x4_t*>(sb + w_row0 + j * 32 * RBW + ((cw ^ xw) << 4));
+    }
   };
+  f32x16_t acc[TI][TJ];
+  auto mma = [&](int s) {  // K step s of a stage
+    const int buf = s & 1;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      bf16x8_t w;
+      if constexpr (W8) {
+        const u32x4_t& r = wraw[(s >> 1) & 1][j];
+        w = (s & 1) ? fp8x8_to_bf16(r[2], r[3]) : fp8x8_to_bf16(r[0], r[1]);
+      } else {
+        w = bw[buf][j];
+      }
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+        acc[i][j] = kSwap ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, af[buf][i], acc[i][j], 0, 0, 0)
+                          : __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[buf][i], w, acc[i][j], 0, 0, 0);
+    }
+  };
+  // LDS reads issued by frag(s)
+  auto nreads = [](int s) { return TI + (W8 ? ((s & 1) == 0 ? TJ : 0) : TJ); };
 
   int q = 0;  // global stage counter (ring position)
-  int tm = ld_m, tn = ld_n;  // tile being computed
   for (int r = 0; r < my_tiles; ++r) {
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -731,15 +813,21 @@ __global__ __launch_bounds__(64 * WGM * WGN, 4) void gemm_bf16_pers_kernel(GemmA
       for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-    // fragment buffer 1 starts at zero: the first stage's "deferred" MFMAs add 0
+    // the operands of the first stage's "deferred" step start at zero: its
+    // MFMAs add 0 (fp8 code 0 is +0)
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int t = 0; t < 8; ++t) af[1][i][t] = static_cast<__bf16>(0.f);
 #pragma unroll
-    for (int j = 0; j < TJ; ++j)
+    for (int j = 0; j < TJ; ++j) {
+      if constexpr (W8) {
+        wraw[1][j] = (u32x4_t){0u, 0u, 0u, 0u};
+      } else {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) bw[1][j][t] = static_cast<__bf16>(0.f);
+        for (int t = 0; t < 8; ++t) bw[1][j][t] = static_cast<__bf16>(0.f);
+      }
+    }
     for (int kt = 0; kt < nk; ++kt, ++q) {
       // this wave's loads of stage q have landed once at most the younger
       // stages' loads are outstanding (vector memory completes in issue order)
@@ -755,28 +843,58 @@ __global__ __launch_bounds__(64 * WGM * WGN, 4) void gemm_bf16_pers_kernel(GemmA
       // step (deferred past the barrier) covers their latency; then each
       // step's MFMAs interleave one-for-one with the reads of the next step
       frag(sb, 0, 0);
-      mma(1);
+      mma(KS - 1);
 #pragma unroll
       for (int s = 0; s + 1 < KS; ++s) {
         frag(sb, s + 1, (s + 1) & 1);
-        mma(s & 1);
+        mma(s);
       }
 #pragma unroll
-      for (int k = 0; k < TI + TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int k = 0; k < nreads(0); ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
       for (int k = 0; k < TI * TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 #pragma unroll
       for (int s = 0; s + 1 < KS; ++s) {
 #pragma unroll
         for (int k = 0; k < TI * TJ; ++k) {
-          if (k < TI + TJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (k < nreads(s + 1)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
 #pragma unroll
-        for (int k = TI * TJ; k < TI + TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int k = TI * TJ; k < nreads(s + 1); ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     }
-    mma(1);
+    mma(KS - 1);
+    if constexpr (W8) {
+      // row n of W stands for code * w_scale[n]: scale the accumulators
+      if constexpr (kSwap) {
+        // the lane's four consecutive W rows 8q + 4hb .. + 3 of block j; a
+        // clamped (past-the-end) group reads in-bounds scales of outputs that
+        // are never stored
+        const int64_t nrows = EPI == EPI_GEGLU ? 2 * static_cast<int64_t>(g.N) : g.N;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t r0 = min(mfma_w_row<BN, TT::WN, EPI>(g, tn, wn * TT::WN + j * 32 + 8 * q + 4 * hb),
+                                   nrows - 4);
+            const f32x4_t sc = *reinterpret_cast<const f32x4_t*>(g.w_scale + r0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+              for (int i = 0; i < TI; ++i) acc[i][j][4 * q + t] *= sc[t];
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          const float sc = g.w_scale[mfma_w_row<BN, TT::WN, EPI>(g, tn, wn * TT::WN + j * 32 + l32)];
+#pragma unroll
+          for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] *= sc;
+        }
+      }
+    }
     if constexpr (kSwap)
       pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, tm * BM, tn, wm, wn, l32, hb);
     else
@@ -802,10 +920,10 @@ int num_cus() {
   return n;
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT>
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8, int EPI, typename OutT>
 void launch_pers_kernel(const GemmArgs& g, hipStream_t st) {
-  constexpr int lds = NS * DTile<BM, BN, WGM, WGN, NS, BK>::STAGE_BYTES;
-  auto kern = gemm_bf16_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI, OutT>;
+  constexpr int lds = NS * PTile<BM, BN, WGM, WGN, NS, BK, W8>::STAGE_BYTES;
+  auto kern = gemm_bf16_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI, OutT>;
   static bool attr_set = false;
   if (!attr_set) {
     hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -813,33 +931,32 @@ void launch_pers_kernel(const GemmArgs& g, hipStream_t st) {
               "gemm: LDS attribute");
     attr_set = true;
   }
-  const int tiles_n = EPI == EPI_GEGLU ? g.N / (BN / 2) : g.N / BN;
+  const int tiles_n = EPI == EPI_GEGLU ? (g.N + BN / 2 - 1) / (BN / 2) : (g.N + BN - 1) / BN;
   const int64_t tiles = static_cast<int64_t>(tiles_n) * ((g.M + BM - 1) / BM);
   require(tiles < (int64_t{1} << 30), "gemm: too many tiles");
-  // workgroups resident per CU: bounded by the 160 KB of LDS and by 16 waves
-  // (4 per SIMD at <= 128 VGPRs); several per CU let one workgroup's
-  // barriers and epilogue overlap another's MFMAs
-  constexpr int occ = std::max(1, std::min(163840 / lds, 16 / (WGM * WGN)));
+  constexpr int occ = pers_occupancy<BM, BN, WGM, WGN, NS, BK, W8>();
   const int grid = static_cast<int>(std::min<int64_t>(tiles, int64_t{occ} * num_cus()));
   kern<<<grid, 64 * WGM * WGN, lds, st>>>(g);
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int BK>
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8>
 void launch_pers(const GemmArgs& g, hipStream_t st) {
   const bool bf = g.out_dtype == DT_BF16;
   switch (g.epi) {
     case EPI_STORE:
-      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_STORE, bf16_t>(g, st)
-         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_STORE, float>(g, st);
+      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_STORE, bf16_t>(g, st)
+         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_STORE, float>(g, st);
       break;
-    case EPI_RESID: launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_RESID, float>(g, st); break;
+    case EPI_RESID:
+      launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_RESID, float>(g, st);
+      break;
     case EPI_ROPE:
-      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_ROPE, bf16_t>(g, st)
-         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_ROPE, float>(g, st);
+      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_ROPE, bf16_t>(g, st)
+         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_ROPE, float>(g, st);
       break;
     default:
-      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_GEGLU, bf16_t>(g, st)
-         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, EPI_GEGLU, float>(g, st);
+      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_GEGLU, bf16_t>(g, st)
+         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_GEGLU, float>(g, st);
       break;
   }
 }
@@ -895,17 +1012,19 @@ void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
 #ifndef SJH_GEMM_PERS
 #define SJH_GEMM_PERS 256, 256, 4, 4, 2, 64
 #endif
-constexpr int kPersTile[] = {SJH_GEMM_PERS};
-constexpr int kPersBN = kPersTile[1];
+// fp8 weights: 48 KB stages (bf16 A rows, fp8 W rows), three in the ring; 8 waves
+// of 128 x 64 (one workgroup per CU, 256 VGPRs per wave)
+#define SJH_GEMM_PERS_FP8 256, 256, 2, 4, 3, 64
+
+// The persistent kernel's epilogues write 8- and 16-byte vectors.
+bool pers_ok(const GemmArgs& g) {
+  return g.N % 4 == 0 && g.ldo % 4 == 0 && g.ldx % 4 == 0 && aligned16(g.out) &&
+         aligned16(g.X) && aligned16(g.bias) && aligned16(g.rope_cos) && aligned16(g.rope_sin);
+}
 
 void launch_mfma(const GemmArgs& g, hipStream_t st) {
-  // persistent kernel: N a multiple of the tile's output width (256, GEGLU
-  // 128) and 16-byte aligned rows for its vector epilogue
-  const bool pers = g.N % (g.epi == EPI_GEGLU ? kPersBN / 2 : kPersBN) == 0 && g.ldo % 4 == 0 &&
-                    g.ldx % 4 == 0 && aligned16(g.out) && aligned16(g.X) && aligned16(g.bias) &&
-                    aligned16(g.rope_cos) && aligned16(g.rope_sin);
-  if (g.M >= 4096 && pers)
-    launch_pers<SJH_GEMM_PERS>(g, st);
+  if (g.M >= 4096 && pers_ok(g))
+    launch_pers<SJH_GEMM_PERS, false>(g, st);
   else if (g.M >= 4096 && (g.epi != EPI_GEGLU || g.N % 128 == 0))
     launch_mfma_epi<SJH_GEMM_BIG>(g, st);
   else if (g.M >= 1024)
@@ -1118,6 +1237,20 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
     default:
       fail("gemm: unknown epilogue");
   }
+  if (g.w_dtype == DT_FP8) {
+    // fp8 weights: the persistent kernel only (16-byte fp8 rows chunks)
+    require(g.in_dtype == DT_BF16, "gemm: fp8 weights need bf16 activations");
+    require(g.w_scale && aligned16(g.w_scale), "gemm: fp8 weights need per-row scales");
+    require(g.K % 64 == 0 && g.lda % 8 == 0 && g.ldw % 16 == 0 && aligned16(g.A) &&
+                aligned16(g.W),
+            "gemm: fp8 weights need K % 64 == 0 and 16-byte aligned rows");
+    require(pers_ok(g), "gemm: fp8 weights need N % 4 == 0 and 16-byte aligned outputs");
+    require(g.epi != EPI_ROPE || g.head_dim == 64, "gemm: fp8 RoPE epilogue needs head_dim 64");
+    launch_pers<SJH_GEMM_PERS_FP8, true>(g, st);
+    check_launch("gemm_fp8w");
+    return;
+  }
+  require(g.w_dtype == DT_BF16 || g.w_dtype == DT_F32, "gemm: unknown weight type");
   const bool mfma = g.in_dtype == DT_BF16 && g.K % kBK == 0 && g.lda % 8 == 0 &&
                     g.ldw % 8 == 0 && aligned16(g.A) && aligned16(g.W) &&
                     (g.epi != EPI_ROPE || g.head_dim == 64) &&

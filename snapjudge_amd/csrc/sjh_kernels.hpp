@@ -10,7 +10,7 @@
 
 namespace sjh {
 
-enum DType : int { DT_F32 = 0, DT_BF16 = 1 };
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_FP8 = 2 };  // DT_FP8: OCP e4m3fn, GEMM weights only
 
 // GEMM epilogues, applied to an fp32 tile staged in LDS.
 enum Epi : int {
@@ -28,7 +28,11 @@ struct GemmArgs {
   const void* W = nullptr;
   int64_t ldw = 0;
   int M = 0, N = 0, K = 0;
-  int in_dtype = DT_BF16;  // A and W
+  int in_dtype = DT_BF16;  // A (and W unless w_dtype says otherwise)
+  // DT_FP8: W holds e4m3 codes and row n of W stands for code * w_scale[n]
+  // (A stays bf16); the scale multiplies the fp32 accumulator.
+  int w_dtype = DT_BF16;
+  const float* w_scale = nullptr;
   int epi = EPI_STORE;
   void* out = nullptr;  // STORE / ROPE / GEGLU
   int64_t ldo = 0;
