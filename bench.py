@@ -23,7 +23,11 @@ forward replayed as a captured hipGraph).  Also reported:
                    latency, hipGraph replay, p50 of 50 (--no-latency skips it);
   cpu_baseline  -- the reference's own CPU forward (oracle/_ref, compiled
                    from its sources, no-BLAS build) on a bounded sample of the
-                   same workload, extrapolated by layers.
+                   same workload, extrapolated by layers;
+  other_configs -- configs 4 (batch 4 x seq 8192) and 5 (28-layer/1024
+                   encoder with fp8 e4m3 weights, batch 32 x seq 1024): valid
+                   tokens/s and per-kernel times, same method (--no-cfg4 /
+                   --no-cfg5 skip them).
 """
 from __future__ import annotations
 
@@ -99,6 +103,64 @@ def cpu_baseline(w, rl, enc, ids, mask, lens, layers_full):
                       f"{layers_full} layers: {secs:.1f} s, extrapolated x{layers_full / nl:g}"}
 
 
+def encoder_leg(sj, torch, model, ids, lens, D, steps, warmup, stream):
+    """Time `steps` encoder forwards (graph replay) on ids already in HBM, then
+    the same steps launch by launch with per-kernel events.  Returns
+    (ms per step, valid tokens/s, per-kernel totals)."""
+    B = len(lens)
+    T = int(lens.sum())
+    packed = np.concatenate([ids[b, :lens[b]] for b in range(B)]).astype(np.int32)
+    d_ids = torch.from_numpy(packed).cuda()
+    d_out = torch.empty((T, D), dtype=torch.float32, device="cuda")
+    lens32 = lens.astype(np.int32)
+
+    def step():
+        model.encode_device(d_ids.data_ptr(), lens32, d_out.data_ptr(), stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    model.profile(True)  # per-launch events (graph replay is off while profiling)
+    step()  # first launch-by-launch step, not counted
+    torch.cuda.synchronize()
+    model.profile(False)
+    model.profile(True)  # restarts the totals
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    prof = model.profile_read()
+    model.profile(False)
+    return elapsed * 1e3 / steps, T * steps / elapsed, prof
+
+
+def extra_leg(sj, torch, name, preset, precision, B, S, lo, hi, steps, stream):
+    """BASELINE config 4 or 5 (encoder tokens/s; not the headline line)."""
+    from snapjudge_amd import synth
+
+    rl, enc, w = synth.make_model(**synth.PRESETS[preset], seed=0)
+    cfg = synth.flat_cfg(rl, enc)
+    D, F, NL = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
+    ids, _, lens = synth.make_batch(B, S, lo, hi, cfg["vocab_size"], seed=1)
+    model = sj.Model(w, cfg, precision=precision, use_graphs=True)
+    del w
+    ms, tps, prof = encoder_leg(sj, torch, model, ids, lens, D, steps, 2, stream)
+    model.close()
+    T = int(lens.sum())
+    gemm_ms = sum(prof[n][0] for n in GEMM_NAMES if n in prof)
+    attn_ms = prof.get("attention", (0.0, 0))[0]
+    attn_fl = NL * 4.0 * D * float((lens.astype(np.float64) ** 2).sum())
+    return {"workload": name, "valid_tokens_per_step": T, "ms_per_step": round(ms, 3),
+            "valid_tokens_per_s": round(tps, 1),
+            "gemm_tflops": round(gemm_flops_per_token(D, F, NL) * T * steps / (gemm_ms / 1e3) / 1e12, 2),
+            "attention_tflops": round(attn_fl * steps / (attn_ms / 1e3) / 1e12, 2) if attn_ms else None,
+            "kernel_ms_per_step": {k: round(v[0] / steps, 4) for k, v in sorted(prof.items())}}
+
+
 def copy_probe(mib):
     """Plain device-to-device copy of a known size (torch's copy kernel): the
     calibration run for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -121,6 +183,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-latency", action="store_true",
                     help="skip the config-2 (batch 1) latency leg")
+    ap.add_argument("--no-cfg4", action="store_true", help="skip the config-4 (S=8192) leg")
+    ap.add_argument("--no-cfg5", action="store_true", help="skip the config-5 (fp8) leg")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run a plain copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -148,36 +212,10 @@ def main():
     # hipEvent pair around every launch on the model's stream, gives the
     # per-kernel durations the roofline uses; it is not part of `value`.
     model = sj.Model(w, cfg, precision=sj.SJH_PREC_BF16, use_graphs=True)
-    packed = np.concatenate([ids[b, :lens[b]] for b in range(B)]).astype(np.int32)
-    d_ids = torch.from_numpy(packed).cuda()
-    d_out = torch.empty((T, D), dtype=torch.float32, device="cuda")
-    lens32 = lens.astype(np.int32)
     stream = torch.cuda.current_stream().cuda_stream
-
-    def step():
-        model.encode_device(d_ids.data_ptr(), lens32, d_out.data_ptr(), stream)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
-    value = T * args.steps / elapsed
-
-    model.profile(True)  # per-launch events (graph replay is off while profiling)
-    step()  # first launch-by-launch step, not counted
-    torch.cuda.synchronize()
-    model.profile(False)
-    model.profile(True)  # restarts the totals
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    prof = model.profile_read()
-    model.profile(False)
+    ms_per_step, value, prof = encoder_leg(sj, torch, model, ids, lens, D, args.steps,
+                                           args.warmup, stream)
+    elapsed = ms_per_step * args.steps / 1e3
 
     # the dominant kernel: the QKV projection GEMM with its fused RoPE epilogue
     # (gemm_bf16_pers_kernel<256,256,4,4,2,64,EPI_ROPE>); algorithmic FLOPs per
@@ -215,6 +253,16 @@ def main():
         p50 = round(float(np.median(lat)), 4)
         lm.close()
 
+    extra = {}
+    if not args.no_cfg4:
+        extra["cfg4"] = extra_leg(sj, torch, "BASELINE config 4: same encoder, batch 4 x seq 8192, "
+                                  "lengths U[4096,8192] seed 1, bf16", "cfg4", sj.SJH_PREC_BF16,
+                                  4, 8192, 4096, 8192, 5, stream)
+    if not args.no_cfg5:
+        extra["cfg5"] = extra_leg(sj, torch, "BASELINE config 5: 28-layer/1024 encoder, GEGLU 2624, "
+                                  "per-row fp8 e4m3 projection weights (bf16 activations), batch "
+                                  "32 x seq 1024, lengths U[256,1024] seed 1", "cfg5",
+                                  sj.SJH_PREC_FP8W, 32, 1024, 256, 1024, 5, stream)
     cpu = None if args.no_cpu else cpu_baseline(w, rl, enc, ids, mask, lens, NL)
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
@@ -242,6 +290,7 @@ def main():
         "padded_tokens_per_s": round(B * S * args.steps / elapsed, 1),
         "kernel_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in sorted(prof.items())},
         "cpu_baseline": cpu,
+        "other_configs": extra,
     }
     print(json.dumps(out), flush=True)
     if args.copy_probe:
