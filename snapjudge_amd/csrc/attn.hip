@@ -2,8 +2,10 @@
 //
 // Fast path (bf16, head_dim 64): one workgroup = (sequence, head, 128
 // queries); 4 waves own 32 queries each.  Key/value tiles of 64 rows move
-// from HBM into a 3-stage LDS ring with direct-to-LDS loads, row-major and
-// XOR-swizzled.  Per tile a wave computes S^T = K . Q^T with
+// from HBM into a 2-stage LDS ring with direct-to-LDS loads, row-major and
+// XOR-swizzled; the ring's 64 KB let two workgroups share a CU, so one
+// workgroup's softmax overlaps the other's MFMAs.  Per tile a wave computes
+// S^T = K . Q^T with
 // v_mfma_f32_32x32x16_bf16 (the query is the MFMA column, so each lane owns
 // one query and 32 of the tile's keys), does the online-softmax update in
 // registers (row max over its own values plus one cross-half exchange; exp2
@@ -34,7 +36,7 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kQ = 128;     // queries per workgroup (4 waves x 32)
 constexpr int kKey = 64;    // keys per tile
-constexpr int kNS = 3;      // LDS ring stages
+constexpr int kNS = 2;      // LDS ring stages (64 KB: two workgroups share a CU)
 constexpr float kLazy = 8.f;  // log2 headroom before the running max is raised
 constexpr int kStage = 2 * kKey * 128;  // bytes per stage: K tile then V tile, 64 x 128 B each
 

@@ -5,6 +5,8 @@
 // One 64-lane wavefront owns one row: the row is read once into registers
 // (coalesced, one float per lane per 64 columns), reduced with cross-lane
 // shuffles, normalised and written once.
+#include <type_traits>
+
 #include "sjh_common.hpp"
 #include "sjh_host.hpp"
 #include "sjh_kernels.hpp"
@@ -90,6 +92,11 @@ template <typename T>
 struct Vec4;
 template <>
 struct Vec4<float> {
+  using Raw = f32x4_t;
+  static __device__ __forceinline__ Raw raw(const float* p) { return *reinterpret_cast<const Raw*>(p); }
+  static __device__ __forceinline__ void cvt(const Raw& v, float (&o)[4]) {
+    o[0] = v[0], o[1] = v[1], o[2] = v[2], o[3] = v[3];
+  }
   static __device__ __forceinline__ void load(const float* p, float (&o)[4]) {
     const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p);
     o[0] = v[0], o[1] = v[1], o[2] = v[2], o[3] = v[3];
@@ -100,6 +107,12 @@ struct Vec4<float> {
 };
 template <>
 struct Vec4<bf16_t> {
+  using Raw = u32x2_t;
+  static __device__ __forceinline__ Raw raw(const bf16_t* p) { return *reinterpret_cast<const Raw*>(p); }
+  static __device__ __forceinline__ void cvt(const Raw& v, float (&o)[4]) {
+    o[0] = __uint_as_float(v[0] << 16), o[1] = __uint_as_float(v[0] & 0xffff0000u);
+    o[2] = __uint_as_float(v[1] << 16), o[3] = __uint_as_float(v[1] & 0xffff0000u);
+  }
   static __device__ __forceinline__ void load(const bf16_t* p, float (&o)[4]) {
     const u32x2_t v = *reinterpret_cast<const u32x2_t*>(p);
     o[0] = __uint_as_float(v[0] << 16), o[1] = __uint_as_float(v[0] & 0xffff0000u);
@@ -110,55 +123,115 @@ struct Vec4<bf16_t> {
   }
 };
 
-template <int NV, typename InT, typename ResT, typename OutT>
+// Residual type of a vector layer norm without a residual input.
+struct NoRes {};
+template <>
+struct Vec4<NoRes> {
+  using Raw = int;
+};
+
+// Sum of a double over the 64 lanes, every lane receiving the total: DPP
+// exchanges inside each row of 16 lanes (pairs, quads, mirrored halves,
+// mirrored rows), then two shuffles across the rows.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(u), CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                        static_cast<uint32_t>(lo));
+}
+__device__ __forceinline__ void wave_sum2(double& a, double& b) {
+  a += dpp_f64<0xB1>(a), b += dpp_f64<0xB1>(b);    // quad_perm [1,0,3,2]
+  a += dpp_f64<0x4E>(a), b += dpp_f64<0x4E>(b);    // quad_perm [2,3,0,1]
+  a += dpp_f64<0x141>(a), b += dpp_f64<0x141>(b);  // row_half_mirror
+  a += dpp_f64<0x140>(a), b += dpp_f64<0x140>(b);  // row_mirror
+  a += __shfl_xor(a, 16, 64), b += __shfl_xor(b, 16, 64);
+  a += __shfl_xor(a, 32, 64), b += __shfl_xor(b, 32, 64);
+}
+
+// Vector variant for D % 4 == 0 and D <= 1024: lane l owns the 4-column
+// chunks l, l + 64, ..., so every row moves with 16-byte (fp32) or 8-byte
+// (bf16) accesses.  FULL: D == 256 * NV, so every chunk exists and a row's
+// loads all go out before the first use.  The statistics are those of
+// src/tensor.cpp:63-71 (mean and population variance in double, inverse std
+// rounded to float), gathered in one pass as the moments of x - x0 (x0 =
+// the row's first value, which keeps E[d^2] - E[d]^2 well conditioned).
+template <int NV, bool FULL, typename InT, typename ResT, typename OutT>
 __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
   const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
+  // The row is uniform over the wave: scalar row addresses and gather index.
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * kLnWaves + (threadIdx.x >> 6));
   if (r >= a.M) return;
   const int D = a.D, nch = D >> 2;
   const int64_t src_row = a.ids ? static_cast<int64_t>(a.ids[r]) : static_cast<int64_t>(r);
   const InT* in = static_cast<const InT*>(a.in) + src_row * a.ld_in;
-  const ResT* res = a.resid ? static_cast<const ResT*>(a.resid) + static_cast<int64_t>(r) * a.ld_in
-                            : nullptr;
-  float v[NV][4];
-  double s = 0.0;
+  constexpr bool kRes = !std::is_same<ResT, NoRes>::value;
+  // Every load of the row (residual, input, gain, bias) is issued before the
+  // first use; raw registers are converted afterwards.
+  float w[NV][4], b[NV][4];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      Vec4<InT>::load(in + 4 * c, v[i]);
-      if (res) {
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[i][k] = 1.f, b[i][k] = 0.f;
+  if (a.normalize && a.w) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (FULL || lane + 64 * i < nch) Vec4<float>::load(a.w + 4 * (lane + 64 * i), w[i]);
+  }
+  if (a.normalize && a.b) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (FULL || lane + 64 * i < nch) Vec4<float>::load(a.b + 4 * (lane + 64 * i), b[i]);
+  }
+  typename Vec4<InT>::Raw vr[NV] = {};
+  typename Vec4<ResT>::Raw tr[NV] = {};
+  if constexpr (kRes) {
+    const ResT* res = static_cast<const ResT*>(a.resid) + static_cast<int64_t>(r) * a.ld_in;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (FULL || lane + 64 * i < nch) tr[i] = Vec4<ResT>::raw(res + 4 * (lane + 64 * i));
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (FULL || lane + 64 * i < nch) vr[i] = Vec4<InT>::raw(in + 4 * (lane + 64 * i));
+  float v[NV][4];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) Vec4<InT>::cvt(vr[i], v[i]);
+  if constexpr (kRes) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (FULL || lane + 64 * i < nch) {
         float t[4];
-        Vec4<ResT>::load(res + 4 * c, t);
+        Vec4<ResT>::cvt(tr[i], t);
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[i][k] += t[k];
       }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) s += static_cast<double>(v[i][k]);
-    } else {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) v[i][k] = 0.f;
-    }
   }
   if (a.xio) {
     float* xo = a.xio + static_cast<int64_t>(r) * a.ld_in;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      if (lane + 64 * i < nch) Vec4<float>::store(xo + 4 * (lane + 64 * i), v[i]);
+      if (FULL || lane + 64 * i < nch) Vec4<float>::store(xo + 4 * (lane + 64 * i), v[i]);
   }
   float inv = 1.f, fmean = 0.f;
   if (a.normalize) {
-    const double mean = wave_sum(s) / static_cast<double>(D);
-    double q = 0.0;
+    const double x0 = static_cast<double>(__builtin_bit_cast(
+        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0][0]))));
+    double s1 = 0.0, s2 = 0.0;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      if (lane + 64 * i < nch)
+      if (FULL || lane + 64 * i < nch)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const double d = static_cast<double>(v[i][k]) - mean;
-          q += d * d;
+          const double d = static_cast<double>(v[i][k]) - x0;
+          s1 += d;
+          s2 += d * d;
         }
-    const double var = wave_sum(q) / static_cast<double>(D);
+    wave_sum2(s1, s2);
+    const double dm = s1 / static_cast<double>(D);
+    const double mean = x0 + dm;
+    const double var = fmax(s2 / static_cast<double>(D) - dm * dm, 0.0);
     inv = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
     fmean = static_cast<float>(mean);
   }
@@ -167,17 +240,14 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + 64 * i;
-    if (c >= nch) continue;
+    if (!FULL && c >= nch) continue;
     float y[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
     if (a.normalize) {
-      float w[4] = {1.f, 1.f, 1.f, 1.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
-      if (a.w) Vec4<float>::load(a.w + 4 * c, w);
-      if (a.b) Vec4<float>::load(a.b + 4 * c, b);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         y[k] = (y[k] - fmean) * inv;
-        if (a.w) y[k] = y[k] * w[k];
-        if (a.b) y[k] = y[k] + b[k];
+        if (a.w) y[k] = y[k] * w[i][k];
+        if (a.b) y[k] = y[k] + b[i][k];
       }
     }
     if (xo) Vec4<float>::store(xo + 4 * c, y);
@@ -188,10 +258,13 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
 template <int NV, typename InT, typename ResT>
 void ln_vec_dispatch_out(const LnArgs& a, hipStream_t st) {
   dim3 grid((a.M + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
+  const bool full = a.D == 256 * NV;
   if (a.y_dtype == DT_BF16)
-    ln_vec_kernel<NV, InT, ResT, bf16_t><<<grid, block, 0, st>>>(a);
+    full ? ln_vec_kernel<NV, true, InT, ResT, bf16_t><<<grid, block, 0, st>>>(a)
+         : ln_vec_kernel<NV, false, InT, ResT, bf16_t><<<grid, block, 0, st>>>(a);
   else
-    ln_vec_kernel<NV, InT, ResT, float><<<grid, block, 0, st>>>(a);
+    full ? ln_vec_kernel<NV, true, InT, ResT, float><<<grid, block, 0, st>>>(a)
+         : ln_vec_kernel<NV, false, InT, ResT, float><<<grid, block, 0, st>>>(a);
 }
 
 template <typename InT, typename ResT>
@@ -311,13 +384,12 @@ void launch_ln(const LnArgs& a, hipStream_t st) {
                    a.ld_y % 4 == 0 && al(a.in, a.in_dtype) && al(a.resid, a.resid_dtype) &&
                    al(a.xio, DT_F32) && al(a.x_out, DT_F32) && al(a.y_out, a.y_dtype) &&
                    al(a.w, DT_F32) && al(a.b, DT_F32);
-  if (vec) {
-    if (a.in_dtype == DT_BF16)
-      a.resid_dtype == DT_BF16 ? ln_vec_dispatch<bf16_t, bf16_t>(a, st)
-                               : ln_vec_dispatch<bf16_t, float>(a, st);
-    else
-      a.resid_dtype == DT_BF16 ? ln_vec_dispatch<float, bf16_t>(a, st)
-                               : ln_vec_dispatch<float, float>(a, st);
+  if (vec && a.resid == nullptr) {
+    a.in_dtype == DT_BF16 ? ln_vec_dispatch<bf16_t, NoRes>(a, st)
+                          : ln_vec_dispatch<float, NoRes>(a, st);
+  } else if (vec && a.in_dtype == DT_F32) {
+    a.resid_dtype == DT_BF16 ? ln_vec_dispatch<float, bf16_t>(a, st)
+                             : ln_vec_dispatch<float, float>(a, st);
   } else if (a.in_dtype == DT_BF16) {
     ln_dispatch_res<bf16_t>(a, st);
   } else {

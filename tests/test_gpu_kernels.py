@@ -144,6 +144,24 @@ def test_add_ln(orc, D, dtype):
             assert float(np.abs(host(Y) - want).max()) <= tol
 
 
+@pytest.mark.parametrize("D", [768, 1000])
+def test_ln_large_offset(orc, D):
+    # rows far from zero with a small spread: the statistics must not lose
+    # the variance to cancellation (the oracle takes two passes in double)
+    rng = np.random.default_rng(D + 1)
+    M = 64
+    x = (rng.standard_normal((M, D)) * 1e-2 + rng.uniform(-3e3, 3e3, size=(M, 1))).astype(np.float32)
+    x[3] = 7.0  # constant row: variance 0, output = bias
+    x[5, 0] += 50.0  # an outlier in the first column
+    w, b = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    X, Wt, Bt = dev(x, torch.float32), dev(w, torch.float32), dev(b, torch.float32)
+    Y = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    call(sj.lib().sjh_add_ln, P(X), P(X), P(Wt), P(Bt), P(Y), M, D, C.c_float(1e-5),
+         0, 1, F32, stream())
+    want = orc.layer_norm(x, w, b, 1e-5)
+    assert float(np.abs(host(Y) - want).max()) <= 2e-4
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_rope(orc, dtype):
     rng = np.random.default_rng(3)
