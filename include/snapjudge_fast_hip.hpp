@@ -28,7 +28,9 @@ class FastSnapjudge {
  public:
   FastSnapjudge(DecisionModel* model, int max_len, bool use_graphs = true);
   // Numerics mode: precision 0 = fp32 parity path, 1 = bf16 MFMA path (the
-  // three-argument constructor's choice); pad_rows 1 also computes the padded
+  // three-argument constructor's choice), 2 = bf16 path with the encoder
+  // projections quantized once to per-row fp8 e4m3 (SJH_PREC_FP8W in
+  // snapjudge_hip.h); pad_rows 1 also computes the padded
   // query rows, as the reference does, so encode() returns them too.
   FastSnapjudge(DecisionModel* model, int max_len, bool use_graphs, int precision, int pad_rows);
   ~FastSnapjudge();
