@@ -13,6 +13,7 @@
 // parity mode and the shapes the MFMA tiling does not cover (tiny models, the
 // scorer's N = 1 projection, LoRA ranks).
 #include <algorithm>
+#include <type_traits>
 
 #include "sjh_common.hpp"
 #include "sjh_host.hpp"
@@ -672,6 +673,8 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
   // its 16-byte accesses span 32 rows, which costs more than it saves where
   // the epilogue also reads (X, RoPE tables).
   constexpr bool kSwap = EPI == EPI_GEGLU;
+  // half units need an even number of wave rows (the lower half computes)
+  constexpr bool kHalves = WGM % 2 == 0;
   extern __shared__ __attribute__((aligned(16))) char dsmem[];
 
   const int tiles_n = EPI == EPI_GEGLU ? (g.N + BN / 2 - 1) / (BN / 2) : (g.N + BN - 1) / BN;
@@ -682,15 +685,30 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
   // fastest) is cut into 8 contiguous ranges, one per XCD, sized by the
   // number of workgroups on that XCD, so the tiles sharing an A row panel stay
   // in one L2; workgroup k of an XCD takes local tiles k, k + c, k + 2c, ...
+  // When the range leaves a last, partial round of r <= c/2 tiles, those
+  // tiles are cut into 2r half units of BM/2 rows, one per workgroup, so the
+  // last round takes about half a tile's time instead of a whole one (in a
+  // half unit the waves of the lower half of the tile do the MFMAs and the
+  // epilogue; the others only share the loads and barriers).
   const int nwg = gridDim.x, xcd = blockIdx.x & 7, xk = blockIdx.x >> 3;
   const int per = nwg >> 3, rem = nwg & 7;
   const int cx = per + (xcd < rem ? 1 : 0);
   const int offx = xcd * per + min(xcd, rem);
   const int lo = static_cast<int>(static_cast<int64_t>(tiles) * offx / nwg);
   const int hi = static_cast<int>(static_cast<int64_t>(tiles) * (offx + cx) / nwg);
-  const int my_tiles = xk < hi - lo ? (hi - lo - xk + cx - 1) / cx : 0;
-  if (my_tiles == 0) return;
-  const int total = my_tiles * nk;
+  const int full_x = (hi - lo) / cx, rem_x = (hi - lo) - full_x * cx;
+  const bool halves = kHalves && full_x >= 1 && rem_x > 0 && 2 * rem_x <= cx;
+  const int my_full = halves ? full_x : (xk < hi - lo ? (hi - lo - xk + cx - 1) / cx : 0);
+  const int my_units = my_full + (halves && xk < 2 * rem_x ? 1 : 0);
+  if (my_units == 0) return;
+  const int total = my_units * nk;
+  // unit u of this workgroup: its tile (m, n) and half (-1: the whole tile)
+  auto unit = [&](int u, int& m, int& n, int& h) {
+    const int t = u < my_full ? lo + xk + u * cx : lo + full_x * cx + (xk >> 1);
+    h = u < my_full ? -1 : (xk & 1);
+    m = t / tiles_n;
+    n = t - m * tiles_n;
+  };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
@@ -698,19 +716,10 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
   const char* A = static_cast<const char*>(g.A);
   const char* W = static_cast<const char*>(g.W);
 
-  // Load cursor (uniform): tile (ld_m, ld_n) of this workgroup's list and K
-  // step ld_kt.
-  int ld_kt = 0, ld_m, ld_n;
-  {
-    const int t0 = lo + xk;
-    ld_m = t0 / tiles_n;
-    ld_n = t0 - ld_m * tiles_n;
-  }
-  const int step_m = cx / tiles_n, step_n = cx - step_m * tiles_n;
-  // compute cursor: the tile whose stages are consumed; taken before the
-  // prologue, whose loads move the load cursor past the first tile when a
-  // tile has fewer K steps than the ring has stages in flight
-  int tm = ld_m, tn = ld_n;
+  // Load cursor (uniform): unit ld_u of this workgroup's list (tile (ld_m,
+  // ld_n), half ld_h) and K step ld_kt.
+  int ld_kt = 0, ld_u = 0, ld_m, ld_n, ld_h;
+  unit(0, ld_m, ld_n, ld_h);
   // Per-lane source rows of the load tile, recomputed only when the cursor
   // enters a new tile; each stage then adds its K offset.  The LDS target of
   // each load instruction is wave-uniform and kept in scalar registers.
@@ -726,7 +735,9 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
       if (gi < TT::GA) {
         const int row = TT::RPIA * gi + lane / TT::CPRA;
         const int chunk = (lane % TT::CPRA) ^ TT::swz(RBA, row);
-        src[i] = A + static_cast<int64_t>(min(ld_m * BM + row, g.M - 1)) * g.lda * 2 + chunk * 16;
+        // a half unit stages its BM/2 rows twice (the copy is never read)
+        const int arow = ld_h < 0 ? row : (row & (BM / 2 - 1)) + (BM / 2) * ld_h;
+        src[i] = A + static_cast<int64_t>(min(ld_m * BM + arow, g.M - 1)) * g.lda * 2 + chunk * 16;
       } else {
         const int row = TT::RPIW * (gi - TT::GA) + lane / TT::CPRW;
         const int chunk = (lane % TT::CPRW) ^ TT::swz(RBW, row);
@@ -741,15 +752,12 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < G; ++i)
       load_lds16(static_cast<const void*>(src[i] + ld_kt * kbytes[i]), base + NW * i * 1024);
-    if (++ld_kt == nk) {  // next tile of the list: index + cx
+    if (++ld_kt == nk) {  // next unit of the list
       ld_kt = 0;
-      ld_n += step_n;
-      ld_m += step_m;
-      if (ld_n >= tiles_n) {
-        ld_n -= tiles_n;
-        ++ld_m;
+      if (++ld_u < my_units) {
+        unit(ld_u, ld_m, ld_n, ld_h);
+        set_src();
       }
-      set_src();
     }
   };
 #pragma unroll
@@ -785,6 +793,7 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
     }
   };
   f32x16_t acc[TI][TJ];
+  const int wm_s = __builtin_amdgcn_readfirstlane(wm);
   auto mma = [&](int s) {  // K step s of a stage
     const int buf = s & 1;
 #pragma unroll
@@ -806,7 +815,11 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
   auto nreads = [](int s) { return TI + (W8 ? ((s & 1) == 0 ? TJ : 0) : TJ); };
 
   int q = 0;  // global stage counter (ring position)
-  for (int r = 0; r < my_tiles; ++r) {
+  for (int r = 0; r < my_units; ++r) {
+    int tm, tn, th;  // compute cursor: the unit whose stages are consumed
+    unit(r, tm, tn, th);
+    // waves with no rows in a half unit only share the loads and barriers
+    const bool idle = th >= 0 && wm_s >= WGM / 2;
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -828,43 +841,51 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
         for (int t = 0; t < 8; ++t) bw[1][j][t] = static_cast<__bf16>(0.f);
       }
     }
-    for (int kt = 0; kt < nk; ++kt, ++q) {
-      // this wave's loads of stage q have landed once at most the younger
-      // stages' loads are outstanding (vector memory completes in issue order)
-      if (q + NS - 2 < total)
-        wait_vmcnt<G * (NS - 2)>();
-      else
-        wait_vmcnt<0>();
-      wait_lgkm0();
-      __builtin_amdgcn_s_barrier();
-      if (q + NS - 1 < total) issue_next((q + NS - 1) % NS);
-      const char* sb = dsmem + (q % NS) * TT::STAGE_BYTES;
-      // operand reads of step 0 go out first; the previous stage's last K
-      // step (deferred past the barrier) covers their latency; then each
-      // step's MFMAs interleave one-for-one with the reads of the next step
-      frag(sb, 0, 0);
-      mma(KS - 1);
+    auto kloop = [&](auto busy) {
+      for (int kt = 0; kt < nk; ++kt, ++q) {
+        // this wave's loads of stage q have landed once at most the younger
+        // stages' loads are outstanding (vector memory completes in issue order)
+        if (q + NS - 2 < total)
+          wait_vmcnt<G * (NS - 2)>();
+        else
+          wait_vmcnt<0>();
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();
+        if (q + NS - 1 < total) issue_next((q + NS - 1) % NS);
+        if constexpr (!decltype(busy)::value) continue;
+        const char* sb = dsmem + (q % NS) * TT::STAGE_BYTES;
+        // operand reads of step 0 go out first; the previous stage's last K
+        // step (deferred past the barrier) covers their latency; then each
+        // step's MFMAs interleave one-for-one with the reads of the next step
+        frag(sb, 0, 0);
+        mma(KS - 1);
 #pragma unroll
-      for (int s = 0; s + 1 < KS; ++s) {
-        frag(sb, s + 1, (s + 1) & 1);
-        mma(s);
-      }
-#pragma unroll
-      for (int k = 0; k < nreads(0); ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-      for (int k = 0; k < TI * TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-#pragma unroll
-      for (int s = 0; s + 1 < KS; ++s) {
-#pragma unroll
-        for (int k = 0; k < TI * TJ; ++k) {
-          if (k < nreads(s + 1)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        for (int s = 0; s + 1 < KS; ++s) {
+          frag(sb, s + 1, (s + 1) & 1);
+          mma(s);
         }
 #pragma unroll
-        for (int k = TI * TJ; k < nreads(s + 1); ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int k = 0; k < nreads(0); ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int k = 0; k < TI * TJ; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+        for (int s = 0; s + 1 < KS; ++s) {
+#pragma unroll
+          for (int k = 0; k < TI * TJ; ++k) {
+            if (k < nreads(s + 1)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          }
+#pragma unroll
+          for (int k = TI * TJ; k < nreads(s + 1); ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
       }
+      if constexpr (decltype(busy)::value) mma(KS - 1);
+    };
+    if (idle) {
+      kloop(std::false_type{});
+      continue;
     }
-    mma(KS - 1);
+    kloop(std::true_type{});
     if constexpr (W8) {
       // row n of W stands for code * w_scale[n]: scale the accumulators
       if constexpr (kSwap) {
@@ -895,16 +916,11 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
         }
       }
     }
+    const int m0 = tm * BM + (th < 0 ? 0 : (BM / 2) * th);
     if constexpr (kSwap)
-      pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, tm * BM, tn, wm, wn, l32, hb);
+      pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wm, wn, l32, hb);
     else
-      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, tm * BM, tn, wm, wn, l32, hb);
-    tn += step_n;
-    tm += step_m;
-    if (tn >= tiles_n) {
-      tn -= tiles_n;
-      ++tm;
-    }
+      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wm, wn, l32, hb);
   }
 }
 

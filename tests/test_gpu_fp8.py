@@ -50,8 +50,10 @@ def test_device_decodes_every_code():
     assert np.array_equal(out, TABLE[q].T)
 
 
+# (23000, 768, 64): 270 tiles on 256 workgroups, so the last round runs as
+# half-row units
 @pytest.mark.parametrize("M,N,K,act,bias", [(1000, 3072, 1024, 0, False), (257, 1024, 2624, 1, True),
-                                            (4500, 256, 64, 2, True)])
+                                            (4500, 256, 64, 2, True), (23000, 768, 64, 1, True)])
 def test_gemm_fp8w_vs_dequantized_fp32(M, N, K, act, bias):
     rng = np.random.default_rng(M)
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)

@@ -259,6 +259,62 @@ def test_gemm_qkv_rope(orc, M):
     assert rel_err(host(Q), want) < 8e-3
 
 
+def _half_units(tiles: int, nwg: int) -> int:
+    # half units the persistent GEMM's static schedule makes: per XCD, a last
+    # partial round of r <= c/2 tiles becomes 2r half-row units
+    n = 0
+    for x in range(8):
+        per, rem = nwg // 8, nwg % 8
+        cx = per + (1 if x < rem else 0)
+        off = x * per + min(x, rem)
+        lo, hi = tiles * off // nwg, tiles * (off + cx) // nwg
+        full, r = divmod(hi - lo, cx)
+        if full >= 1 and 0 < r and 2 * r <= cx:
+            n += 2 * r
+    return n
+
+
+@pytest.mark.parametrize("kind", ["store", "resid", "geglu", "rope"])
+def test_gemm_persistent_half_units(orc, kind):
+    # more tiles than workgroups with a short last round: that round runs as
+    # half-row units (every row of the output checked against the oracle)
+    M, K, H, Dh, L = 23000, 64, 4, 64, 512
+    n = {"store": 768, "resid": 768, "geglu": 384, "rope": 3 * H * Dh}[kind]
+    nw = 2 * n if kind == "geglu" else n
+    tiles = (n // (128 if kind == "geglu" else 256)) * ((M + 255) // 256)
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    halves = _half_units(tiles, min(tiles, ncu))
+    print(f"persistent half units: {kind} M={M} N={n} tiles={tiles} halves={halves}", flush=True)
+    assert halves > 0
+    rng = np.random.default_rng(77)
+    a, w, b = rnd(rng, (M, K)), rnd(rng, (nw, K), 0.1), rnd(rng, n)
+    A, W = dev(a, torch.bfloat16), dev(w, torch.bfloat16)
+    if kind == "store":
+        Bv = dev(b, torch.float32)
+        O = torch.empty((M, n), dtype=torch.bfloat16, device="cuda")
+        call(sj.lib().sjh_gemm, P(A), P(W), P(Bv), P(O), M, n, K, 1, BF, stream())
+        want = orc.gemm_nt(a, w, b, 1)
+        assert rel_err(host(O), want) < 8e-3
+    elif kind == "resid":
+        x0 = rng.standard_normal((M, n)).astype(np.float32)
+        X = dev(x0, torch.float32)
+        call(sj.lib().sjh_gemm_residual, P(A), P(W), P(X), M, n, K, BF, stream())
+        assert float(np.abs(host(X) - (x0 + orc.gemm_nt(a, w))).max()) < 2e-4
+    elif kind == "geglu":
+        O = torch.empty((M, n), dtype=torch.bfloat16, device="cuda")
+        call(sj.lib().sjh_gemm_geglu, P(A), P(W), P(O), M, n, K, BF, stream())
+        assert rel_err(host(O), orc.gemm_geglu(a, w)) < 8e-3
+    else:
+        c, s = orc.rope_table(160000.0, L, Dh)
+        Ct, St = dev(c, torch.float32), dev(s, torch.float32)
+        Pt = torch.from_numpy((np.arange(M) % L).astype(np.int32)).cuda()
+        O = torch.empty((M, n), dtype=torch.bfloat16, device="cuda")
+        call(sj.lib().sjh_gemm_qkv_rope, P(A), P(W), P(O), P(Pt), P(Ct), P(St), L, M, H, Dh, K,
+             BF, stream())
+        want = orc.rope_inplace(orc.gemm_nt(a, w), c, s, L, H, Dh)
+        assert rel_err(host(O), want) < 8e-3
+
+
 def test_gemm_tile_shape_invariance():
     # the tile shape is chosen from M; a row's result must not depend on it
     # (bit-identical for every epilogue)
