@@ -42,10 +42,13 @@ constexpr int kStage = 2 * kKey * 128;  // bytes per stage: K tile then V tile, 
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 typedef __attribute__((ext_vector_type(8))) short s16x8_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
 __device__ __forceinline__ float wave_max32(float v) {
-  // lanes l and l^32 hold the two halves of one query's keys
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  // lanes l and l^32 hold the two halves of one query's keys: one
+  // v_permlane32_swap hands each half the other's value (no LDS round trip)
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Chunk position of 16-byte chunk c of tile row r is c ^ kv_swz(r): 16
@@ -125,32 +128,30 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
     o[0][e] = 0.f;
     o[1][e] = 0.f;
   }
-  float m_i = -INFINITY, l_i = 0.f;
+  // l_i: this lane's share of the softmax denominator, summed from the same
+  // bf16 weights the P.V MFMA consumes (two partial sums, v_dot2 with ones)
+  float m_i = -INFINITY, l_i = 0.f, l_j = 0.f;
   const float c = a.scale * kLog2e;
 
   // LDS offsets (within a stage) of this lane's operand reads, the same for
   // every tile.  K fragments: row jb*32 + l32, dims 16*st + 8*hb + [0, 8).
   // V^T fragments through transposed reads (see lds_read_tr): lane group
   // g = lane / 16 covers dims 16 * (g % 2) + [0, 16) of a 32-dim block and
-  // keys 4 * (g / 2) + [0, 4) of an 8-key half step.
-  int koff[2][4], voff[2][2][2][2];
+  // keys 4 * (g / 2) + [0, 4) of an 8-key half step.  The swizzle key of a
+  // row, (row >> 1) & 7, does not see the 32-row block jb or the 16-row step
+  // u, so those enter as constants (folded into the LDS instructions'
+  // offset fields): koff[st] + 4096 jb, voff[db][hl] + 4096 jb + 2048 u.
+  int koff[4], voff[2][2];
   {
     const int tq = lane & 3, tk = (lane >> 2) & 3, tg = lane >> 4;
     const int tdim = 16 * (tg & 1) + 4 * tq;
     const int tkey = 4 * (tg >> 1) + tk;
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
+    for (int st = 0; st < 4; ++st) koff[st] = kv_off(l32, 16 * st + 8 * hb);
 #pragma unroll
-      for (int st = 0; st < 4; ++st) koff[jb][st] = kv_off(jb * 32 + l32, 16 * st + 8 * hb);
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int hl = 0; hl < 2; ++hl)
-            voff[jb][u][db][hl] =
-                kKey * 128 + kv_off(jb * 32 + 16 * u + 8 * hl + tkey, db * 32 + tdim);
-    }
+      for (int hl = 0; hl < 2; ++hl) voff[db][hl] = kKey * 128 + kv_off(8 * hl + tkey, db * 32 + tdim);
   }
 
   // One 64-key tile at key offset kt from the stage at sb.  MASK: apply the
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
       for (int e = 0; e < 16; ++e) s[jb][e] = 0.f;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(sb + koff[jb][st]);
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(sb + jb * 4096 + koff[st]);
         s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[jb], 0, 0, 0);
       }
     }
@@ -199,6 +200,7 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
       const float alpha = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_new);
       m_i = m_new;
       l_i *= alpha;
+      l_j *= alpha;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         o[0][e] *= alpha;
@@ -210,9 +212,7 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jb][e], c, -m_use));
-        s[jb][e] = p;
-        l_i += p;
+        s[jb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jb][e], c, -m_use));
       }
     // O^T[dim][query] += V^T[dim][key] . P^T[key][query].  The MFMA's k index
     // 8 * hb + t of a 16-key step u stands for key 16u + 4hb + t (t < 4) or
@@ -225,10 +225,15 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
         bf16x8_t pf;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pf[e] = static_cast<__bf16>(s[jb][8 * u + e]);
+        const bf16x2_t ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+        l_i = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[0], pf[1]}, ones, l_i, false);
+        l_j = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[2], pf[3]}, ones, l_j, false);
+        l_i = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[4], pf[5]}, ones, l_i, false);
+        l_j = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[6], pf[7]}, ones, l_j, false);
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
-          const s16x4_t lo = lds_read_tr(sb + voff[jb][u][db][0]);
-          const s16x4_t hi = lds_read_tr(sb + voff[jb][u][db][1]);
+          const s16x4_t lo = lds_read_tr(sb + jb * 4096 + u * 2048 + voff[db][0]);
+          const s16x4_t hi = lds_read_tr(sb + jb * 4096 + u * 2048 + voff[db][1]);
           const bf16x8_t vf = __builtin_bit_cast(
               bf16x8_t, (s16x8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
@@ -256,6 +261,7 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
       tile(std::false_type{}, sb, kt);
   }
 
+  l_i += l_j;
   const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qi < qlen) {
