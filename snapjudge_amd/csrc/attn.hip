@@ -108,17 +108,36 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
   // wave w moves groups w, w + 4, w + 8, w + 12.  Lane l carries row
   // 8 * (group % 8) + l / 8 and lands in chunk slot l % 8, so it reads the
   // logical chunk (l % 8) ^ kv_swz(row).
+  // Groups i = 0, 1 are K rows, 2, 3 V rows.  A full tile adds the lane's
+  // fixed byte offset to a wave-uniform row base; only a tile that runs past
+  // klen clamps its rows one by one.
   const int lrow = lane >> 3, cslot = lane & 7;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t goff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * ((wave + 4 * i) & 7) + lrow;
+    goff[i] = static_cast<uint32_t>(r * (i < 2 ? a.ld_k : a.ld_v) * 2 + ((cslot ^ kv_swz(r)) << 4));
+  }
   auto issue = [&](int t, int buf) {
     char* base = smem + buf * kStage;
+    const int k0 = klo + t * kKey;
+    if (k0 + kKey <= klen) {
+      const char* kb = reinterpret_cast<const char*>(K + (row0 + k0) * a.ld_k);
+      const char* vb = reinterpret_cast<const char*>(V + (row0 + k0) * a.ld_v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int grp = wave + 4 * i;
-      const int r = 8 * (grp & 7) + lrow;
-      const int key = min(klo + t * kKey + r, klen - 1);
-      const bf16_t* src = (grp < 8 ? K + (row0 + key) * a.ld_k : V + (row0 + key) * a.ld_v) +
-                          ((cslot ^ kv_swz(r)) << 3);
-      load_lds16(src, base + grp * 1024);
+      for (int i = 0; i < 4; ++i)
+        load_lds16((i < 2 ? kb : vb) + goff[i], base + (wave_s + 4 * i) * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int grp = wave_s + 4 * i;
+        const int r = 8 * (grp & 7) + lrow;
+        const int key = min(k0 + r, klen - 1);
+        const bf16_t* src = (i < 2 ? K + (row0 + key) * a.ld_k : V + (row0 + key) * a.ld_v) +
+                            ((cslot ^ kv_swz(r)) << 3);
+        load_lds16(src, base + grp * 1024);
+      }
     }
   };
 
@@ -154,11 +173,11 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
       for (int hl = 0; hl < 2; ++hl) voff[db][hl] = kKey * 128 + kv_off(8 * hl + tkey, db * 32 + tdim);
   }
 
-  // One 64-key tile at key offset kt from the stage at sb.  MASK: apply the
-  // key range [qlo, qhi) (last tile, or a sliding window); interior tiles of
-  // full attention skip it.
+  // One 64-key tile at key offset kt from the stage at sb.  MASK 0: interior
+  // tile of full attention; 1: its last tile (keys >= qhi masked); 2: a
+  // sliding window (keys outside [qlo, qhi) masked).
   auto tile = [&](auto mask_tag, const char* sb, int kt) {
-    constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr int MASK = decltype(mask_tag)::value;
     // S^T[key][query] for keys kt + [0, 32) and kt + [32, 64)
     f32x16_t s[2];
 #pragma unroll
@@ -171,7 +190,7 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
         s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[jb], 0, 0, 0);
       }
     }
-    if constexpr (MASK) {
+    if constexpr (MASK != 0) {
       // key of element (jb, e) is kt + 4*hb + 32*jb + 8*(e/4) + e%4
       const int lo = qlo - kt - 4 * hb, hi = qhi - kt - 4 * hb;
 #pragma unroll
@@ -179,7 +198,8 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int k = 32 * jb + 8 * (e >> 2) + (e & 3);
-          s[jb][e] = (k < lo || k >= hi) ? -INFINITY : s[jb][e];
+          const bool out = MASK == 2 ? (k < lo || k >= hi) : k >= hi;
+          s[jb][e] = out ? -INFINITY : s[jb][e];
         }
     }
     // Online softmax in the log2 domain (c = scale * log2 e).  A lane keeps
@@ -245,21 +265,25 @@ __global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
   for (int st = 0; st < kNS - 1; ++st)
     if (st < ntiles) issue(st, st);
 
-  for (int t = 0; t < ntiles; ++t) {
+  auto step = [&](int t, auto mask_tag) {
     if (t + kNS - 2 < ntiles)
       wait_vmcnt<4 * (kNS - 2)>();
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
     if (t + kNS - 1 < ntiles) issue(t + kNS - 1, (t + kNS - 1) % kNS);
-    if (!wave_active) continue;
-    const int kt = klo + t * kKey;
-    const char* sb = smem + (t % kNS) * kStage;
-    if (kt + kKey > khi || a.window > 0)
-      tile(std::true_type{}, sb, kt);
-    else
-      tile(std::false_type{}, sb, kt);
-  }
+    if (wave_active) tile(mask_tag, smem + (t % kNS) * kStage, klo + t * kKey);
+  };
+  // The interior tiles of full attention run in a loop of their own, then the
+  // masked ones: no branch between the two tile bodies inside the hot loop
+  // (such a merge costs register copies of the accumulators on every tile).
+  const int n_plain = a.window > 0 ? 0 : (khi - klo) / kKey;
+  int t = 0;
+  for (; t < n_plain; ++t) step(t, std::integral_constant<int, 0>{});
+  if (a.window > 0)
+    for (; t < ntiles; ++t) step(t, std::integral_constant<int, 2>{});
+  else
+    for (; t < ntiles; ++t) step(t, std::integral_constant<int, 1>{});
 
   l_i += l_j;
   const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
