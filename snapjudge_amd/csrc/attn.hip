@@ -2,9 +2,9 @@
 //
 // Fast path (bf16, head_dim 64): one workgroup = (sequence, head, 128
 // queries); 4 waves own 32 queries each.  Key/value tiles of 64 rows move
-// from HBM into a 2-stage LDS ring with direct-to-LDS loads, row-major and
-// XOR-swizzled; the ring's 64 KB let two workgroups share a CU, so one
-// workgroup's softmax overlaps the other's MFMAs.  Per tile a wave computes
+// from HBM into a 2-stage LDS ring (32 KB) with direct-to-LDS loads,
+// row-major and XOR-swizzled; three workgroups share a CU, so one
+// workgroup's softmax overlaps the others' MFMAs.  Per tile a wave computes
 // S^T = K . Q^T with
 // v_mfma_f32_32x32x16_bf16 (the query is the MFMA column, so each lane owns
 // one query and 32 of the tile's keys), does the online-softmax update in
@@ -36,7 +36,7 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kQ = 128;     // queries per workgroup (4 waves x 32)
 constexpr int kKey = 64;    // keys per tile
-constexpr int kNS = 2;      // LDS ring stages (64 KB: two workgroups share a CU)
+constexpr int kNS = 2;      // LDS ring stages (2 x 16 KB)
 constexpr float kLazy = 8.f;  // log2 headroom before the running max is raised
 constexpr int kStage = 2 * kKey * 128;  // bytes per stage: K tile then V tile, 64 x 128 B each
 
@@ -68,7 +68,10 @@ __device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
       (__attribute__((address_space(3))) s16x4_t*)(p));
 }
 
-__global__ __launch_bounds__(256) void attn_bf16_mfma_kernel(AttnArgs a) {
+// Register budget for three workgroups per CU (168 VGPRs, 3 waves per SIMD):
+// a third wave per SIMD lets softmax VALU work, MFMAs and LDS reads of
+// different waves overlap.
+__global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kNS * kStage];
   const int b = a.seq_order ? a.seq_order[blockIdx.z] : static_cast<int>(blockIdx.z);
   const int h = blockIdx.y;
