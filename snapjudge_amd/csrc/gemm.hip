@@ -148,7 +148,8 @@ __device__ __forceinline__ void consume(const T& v) {
 // Epilogue on the accumulators in registers (see the comment above).
 template <int BM, int BN, int WM, int WN, int TI, int TJ, int EPI, typename OutT>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int m0,
-                                              int tile_n, int wm, int wn, int l32, int hb) {
+                                              int tile_n, int wm, int wn, int l32, int hb,
+                                              const char* rope_tab = nullptr) {
   const int row_base = m0 + wm * WM + 4 * hb;
   if constexpr (EPI == EPI_GEGLU) {
     OutT* out = static_cast<OutT*>(g.out);
@@ -219,18 +220,29 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int e0 = 0; e0 < 16; e0 += RG) {
-        int p[RG];
-#pragma unroll
-        for (int e = 0; e < RG; ++e) {
-          const int m = min(row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3), g.M - 1);
-          p[e] = g.pos[m];
-        }
         float cs[RG], sn[RG];
+        if (rope_tab) {
+          // the unit's table rows, staged in LDS: cos at row * 128, sin 32 KB on
+          const int rl = row_base - m0 + i * 32;
 #pragma unroll
-        for (int e = 0; e < RG; ++e) {
-          const int64_t tb = static_cast<int64_t>(min(max(p[e], 0), g.rope_rows - 1)) * 32 + l32;
-          cs[e] = g.rope_cos[tb];
-          sn[e] = g.rope_sin[tb];
+          for (int e = 0; e < RG; ++e) {
+            const char* t = rope_tab + (rl + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3)) * 128 + l32 * 4;
+            cs[e] = *reinterpret_cast<const float*>(t);
+            sn[e] = *reinterpret_cast<const float*>(t + 32768);
+          }
+        } else {
+          int p[RG];
+#pragma unroll
+          for (int e = 0; e < RG; ++e) {
+            const int m = min(row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3), g.M - 1);
+            p[e] = g.pos[m];
+          }
+#pragma unroll
+          for (int e = 0; e < RG; ++e) {
+            const int64_t tb = static_cast<int64_t>(min(max(p[e], 0), g.rope_rows - 1)) * 32 + l32;
+            cs[e] = g.rope_cos[tb];
+            sn[e] = g.rope_sin[tb];
+          }
         }
 #pragma unroll
         for (int e = 0; e < RG; ++e) {
@@ -615,6 +627,31 @@ __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)
   }
 }
 
+// RoPE tables of a persistent unit's 256 rows staged in LDS for its epilogue,
+// in the ring stage the unit's last K step has just consumed: cos rows at
+// row * 128, sin rows 32 KB on (64 KB).  Loaded with direct-to-LDS copies of
+// whole 128-byte table rows, so the epilogue's per-element table reads are
+// LDS reads instead of one global gather per (row, dim).  Every wave of the
+// workgroup takes part (loads and both barriers).
+__device__ __forceinline__ void rope_stage_lds(const GemmArgs& g, char* tab, int m0, int wave_s,
+                                               int lane) {
+  int p[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int m = min(m0 + 8 * (wave_s + 16 * k) + (lane >> 3), g.M - 1);
+    p[k] = min(max(g.pos[m], 0), g.rope_rows - 1);
+  }
+  __builtin_amdgcn_s_barrier();  // every wave is done with the stage's operands
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float* t = (i >> 1) ? g.rope_sin : g.rope_cos;
+    load_lds16(t + static_cast<int64_t>(p[i & 1]) * 32 + (lane & 7) * 4,
+               tab + (i >> 1) * 32768 + (wave_s + 16 * (i & 1)) * 1024);
+  }
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+}
+
 // Ring geometry of the persistent kernel.  A rows are bf16; W rows are bf16,
 // or fp8 (W8: one byte per element, half the bytes per stage).  Each load
 // instruction fills 1 KB of LDS (64 lanes x 16 bytes): groups [0, GA) are A
@@ -673,6 +710,9 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
   // its 16-byte accesses span 32 rows, which costs more than it saves where
   // the epilogue also reads (X, RoPE tables).
   constexpr bool kSwap = EPI == EPI_GEGLU;
+  // RoPE tables through LDS: needs a 64 KB stage and 16 waves of 256 rows
+  constexpr bool kRopeLds = EPI == EPI_ROPE && !kSwap && BM == 256 && WGM * WGN == 16 &&
+                            PTile<BM, BN, WGM, WGN, NS, BK, W8>::STAGE_BYTES >= 65536;
   // half units need an even number of wave rows (the lower half computes)
   constexpr bool kHalves = WGM % 2 == 0;
   extern __shared__ __attribute__((aligned(16))) char dsmem[];
@@ -881,11 +921,24 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
       }
       if constexpr (decltype(busy)::value) mma(KS - 1);
     };
+    const int m0 = tm * BM + (th < 0 ? 0 : (BM / 2) * th);
+    const char* rope_tab = nullptr;
+    auto stage_tables = [&]() {
+      if constexpr (kRopeLds) {
+        if (tn * BN < 2 * g.rope_dim) {  // uniform: the tile has rotated columns
+          char* tab = dsmem + ((q + NS - 1) % NS) * TT::STAGE_BYTES;  // stage of the last K step
+          rope_stage_lds(g, tab, m0, wave_s, lane);
+          rope_tab = tab;
+        }
+      }
+    };
     if (idle) {
       kloop(std::false_type{});
+      stage_tables();
       continue;
     }
     kloop(std::true_type{});
+    stage_tables();
     if constexpr (W8) {
       // row n of W stands for code * w_scale[n]: scale the accumulators
       if constexpr (kSwap) {
@@ -916,11 +969,11 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
         }
       }
     }
-    const int m0 = tm * BM + (th < 0 ? 0 : (BM / 2) * th);
     if constexpr (kSwap)
       pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wm, wn, l32, hb);
     else
-      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wm, wn, l32, hb);
+      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wm, wn, l32, hb,
+                                                               rope_tab);
   }
 }
 
