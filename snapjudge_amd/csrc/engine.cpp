@@ -490,6 +490,26 @@ void Engine::gemm(const char* name, const GemmArgs& g0, hipStream_t st) {
   prof_end(name, st);
 }
 
+void Engine::resid_gemm_ln(const char* gname, const GemmArgs& g0, const char* lname, LnArgs a,
+                           hipStream_t st) {
+  GemmArgs g = g0;
+  g.partial = splitk_.as<float>();
+  g.partial_cap = static_cast<int64_t>(splitk_.bytes() / 4);
+  prof_begin(st);
+  const int S = g.M <= 256 ? launch_gemm_resid_partials(g, st) : 0;
+  if (S == 0) launch_gemm(g, st);
+  prof_end(gname, st);
+  if (S > 0) {  // X is updated by the layer norm: X += sum of the splits (+ bias)
+    a.parts = g.partial;
+    a.n_parts = S;
+    a.part_stride = static_cast<int64_t>(g.M) * g.N;
+    a.ld_part = g.N;
+    a.part_bias = g.bias;
+    a.xio = g.X;
+  }
+  ln(lname, a, st);
+}
+
 void Engine::ln(const char* name, const LnArgs& a, hipStream_t st) {
   prof_begin(st);
   launch_ln(a, st);
@@ -539,23 +559,40 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
   }
 
   const float scale = 1.0f / std::sqrt(static_cast<float>(Dh_));
+  // Y = attn_norm(X) of layer li (src/model.cpp:347-353; identity copy when
+  // the layer has none)
+  auto attn_norm_args = [&](int li) {
+    const LayerDev& ly = layers_[static_cast<size_t>(li)];
+    LnArgs a;
+    a.in = X;
+    a.in_dtype = DT_F32;
+    a.ld_in = D;
+    a.normalize = ly.has_attn_norm;
+    a.w = ly.has_attn_norm ? ly.attn_norm.as<float>() : nullptr;
+    a.eps = eps_;
+    a.y_out = Y;
+    a.y_dtype = adt;
+    a.ld_y = D;
+    a.M = T;
+    a.D = D;
+    return a;
+  };
+  // final norm, in place (src/model.cpp:400)
+  LnArgs final_args;
+  final_args.in = X;
+  final_args.in_dtype = DT_F32;
+  final_args.ld_in = D;
+  final_args.w = final_norm_.as<float>();
+  final_args.eps = eps_;
+  final_args.x_out = X;
+  final_args.ld_x = D;
+  final_args.M = T;
+  final_args.D = D;
   for (int li = 0; li < nlayers_; ++li) {
     const LayerDev& ly = layers_[static_cast<size_t>(li)];
-    if (ly.has_attn_norm || li > 0) {
-      LnArgs a;
-      a.in = X;
-      a.in_dtype = DT_F32;
-      a.ld_in = D;
-      a.normalize = ly.has_attn_norm;
-      a.w = ly.has_attn_norm ? ly.attn_norm.as<float>() : nullptr;
-      a.eps = eps_;
-      a.y_out = Y;
-      a.y_dtype = adt;
-      a.ld_y = D;
-      a.M = T;
-      a.D = D;
-      ln("attn_norm", a, st);
-    }
+    // layers after the first get their attn_norm from the previous layer's
+    // Wo2 step (resid_gemm_ln)
+    if (li == 0 && ly.has_attn_norm) ln("attn_norm", attn_norm_args(0), st);
     {  // qkv = Y . Wqkv^T with RoPE on q, k (src/model.cpp:355-365)
       GemmArgs g;
       g.A = Y;
@@ -614,9 +651,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.epi = EPI_RESID;
       g.X = X;
       g.ldx = D;
-      gemm("gemm_wo_resid", g, st);
-    }
-    {  // Y = mlp_norm(X) (src/model.cpp:392)
+      // Y = mlp_norm(X) (src/model.cpp:392)
       LnArgs a;
       a.in = X;
       a.in_dtype = DT_F32;
@@ -628,7 +663,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       a.ld_y = D;
       a.M = T;
       a.D = D;
-      ln("mlp_norm", a, st);
+      resid_gemm_ln("gemm_wo_resid", g, "mlp_norm", a, st);
     }
     {  // G = geglu(Y . Wi^T) (src/model.cpp:394)
       GemmArgs g;
@@ -661,21 +696,12 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.epi = EPI_RESID;
       g.X = X;
       g.ldx = D;
-      gemm("gemm_wo2_resid", g, st);
+      // then the next layer's attn_norm, or the final norm
+      if (li + 1 < nlayers_)
+        resid_gemm_ln("gemm_wo2_resid", g, "attn_norm", attn_norm_args(li + 1), st);
+      else
+        resid_gemm_ln("gemm_wo2_resid", g, "final_norm", final_args, st);
     }
-  }
-  {  // final norm, in place (src/model.cpp:400)
-    LnArgs a;
-    a.in = X;
-    a.in_dtype = DT_F32;
-    a.ld_in = D;
-    a.w = final_norm_.as<float>();
-    a.eps = eps_;
-    a.x_out = X;
-    a.ld_x = D;
-    a.M = T;
-    a.D = D;
-    ln("final_norm", a, st);
   }
   if (lora_r_ > 0) {  // h += (h . A^T) . B^T (src/model.cpp:402-407)
     GemmArgs g;

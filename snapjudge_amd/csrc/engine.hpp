@@ -130,6 +130,10 @@ class Engine {
   // launch helpers (record profile events when enabled)
   void gemm(const char* name, const GemmArgs& g, hipStream_t st);
   void ln(const char* name, const LnArgs& a, hipStream_t st);
+  // X += A . W^T followed by the layer norm `a` that reads X: for short
+  // batches the split-K residual epilogue is folded into that layer norm.
+  void resid_gemm_ln(const char* gname, const GemmArgs& g, const char* lname, LnArgs a,
+                     hipStream_t st);
   void attn(const char* name, const AttnArgs& a, hipStream_t st);
   void prof_begin(hipStream_t st);
   void prof_end(const char* name, hipStream_t st);

@@ -1172,12 +1172,12 @@ void launch_splitk_epi(const GemmArgs& g, dim3 grid, hipStream_t st) {
   kern<<<grid, 256, lds, st>>>(g);
 }
 
-// Returns false (caller takes the regular path) when the workspace is too
-// small or K too short to split.
-bool launch_splitk(const GemmArgs& g0, hipStream_t st) {
-  GemmArgs g = g0;
+// Launches the split-K product (partials only) and returns the number of
+// splits, or 0 (nothing launched) when the workspace is too small or K too
+// short to split.
+int launch_splitk_partials(GemmArgs& g, hipStream_t st) {
   g.n_w = g.epi == EPI_GEGLU ? 2 * g.N : g.N;
-  if (g.epi == EPI_GEGLU && g.N % (kSkBN / 2) != 0) return false;
+  if (g.epi == EPI_GEGLU && g.N % (kSkBN / 2) != 0) return 0;
   const int tiles_n = g.epi == EPI_GEGLU ? g.N / (kSkBN / 2) : (g.N + kSkBN - 1) / kSkBN;
   const int tiles = ((g.M + kSkBM - 1) / kSkBM) * tiles_n;
   const int nk = g.K / kBK;
@@ -1186,7 +1186,7 @@ bool launch_splitk(const GemmArgs& g0, hipStream_t st) {
   S = std::min(S, 16);
   g.k_chunk = (nk + S - 1) / S;
   S = (nk + g.k_chunk - 1) / g.k_chunk;
-  if (S < 2 || static_cast<int64_t>(S) * g.M * g.n_w > g.partial_cap) return false;
+  if (S < 2 || static_cast<int64_t>(S) * g.M * g.n_w > g.partial_cap) return 0;
   dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(S));
   switch (g.epi) {
     case EPI_STORE: launch_splitk_epi<EPI_STORE>(g, grid, st); break;
@@ -1195,6 +1195,15 @@ bool launch_splitk(const GemmArgs& g0, hipStream_t st) {
     default: launch_splitk_epi<EPI_GEGLU>(g, grid, st); break;
   }
   check_launch("gemm_splitk");
+  return S;
+}
+
+// Returns false (caller takes the regular path) when the workspace is too
+// small or K too short to split.
+bool launch_splitk(const GemmArgs& g0, hipStream_t st) {
+  GemmArgs g = g0;
+  const int S = launch_splitk_partials(g, st);
+  if (S == 0) return false;
   const int64_t outs = static_cast<int64_t>(g.M) * g.N;
   dim3 eg(static_cast<unsigned>((outs + 255) / 256));
   if (g.out_dtype == DT_BF16 || g.epi == EPI_RESID)
@@ -1279,6 +1288,21 @@ void launch_generic(const GemmArgs& g, hipStream_t st) {
 }
 
 }  // namespace
+
+// The bf16 MFMA kernels' operand requirements.
+bool mfma_ok(const GemmArgs& g) {
+  return g.in_dtype == DT_BF16 && g.w_dtype == DT_BF16 && g.K % kBK == 0 && g.lda % 8 == 0 &&
+         g.ldw % 8 == 0 && aligned16(g.A) && aligned16(g.W) &&
+         (g.epi != EPI_ROPE || g.head_dim == 64) && (g.epi != EPI_GEGLU || g.N % 64 == 0);
+}
+
+int launch_gemm_resid_partials(const GemmArgs& g0, hipStream_t st) {
+  if (g0.epi != EPI_RESID || g0.M <= 0 || g0.M > 256 || g0.N <= 0 || g0.K <= 0 || !g0.partial ||
+      !g0.A || !g0.W || !g0.X || g0.lda < g0.K || g0.ldw < g0.K || g0.ldx < g0.N || !mfma_ok(g0))
+    return 0;
+  GemmArgs g = g0;
+  return launch_splitk_partials(g, st);
+}
 
 void launch_gemm(const GemmArgs& g, hipStream_t st) {
   if (g.M <= 0 || g.N <= 0) return;

@@ -123,10 +123,16 @@ struct Vec4<bf16_t> {
   }
 };
 
-// Residual type of a vector layer norm without a residual input.
+// Residual types of a vector layer norm: none, or the split-K partials of the
+// residual GEMM that produced the input (LnArgs::parts).
 struct NoRes {};
 template <>
 struct Vec4<NoRes> {
+  using Raw = int;
+};
+struct PartsRes {};
+template <>
+struct Vec4<PartsRes> {
   using Raw = int;
 };
 
@@ -166,7 +172,8 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
   const int D = a.D, nch = D >> 2;
   const int64_t src_row = a.ids ? static_cast<int64_t>(a.ids[r]) : static_cast<int64_t>(r);
   const InT* in = static_cast<const InT*>(a.in) + src_row * a.ld_in;
-  constexpr bool kRes = !std::is_same<ResT, NoRes>::value;
+  constexpr bool kParts = std::is_same<ResT, PartsRes>::value;
+  constexpr bool kRes = !std::is_same<ResT, NoRes>::value && !kParts;
   // Every load of the row (residual, input, gain, bias) is issued before the
   // first use; raw registers are converted afterwards.
   float w[NV][4], b[NV][4];
@@ -198,6 +205,46 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
   float v[NV][4];
 #pragma unroll
   for (int i = 0; i < NV; ++i) Vec4<InT>::cvt(vr[i], v[i]);
+  if constexpr (kParts) {
+    // x = in + (p_0 + p_1 + ... + p_{S-1} + bias), summed from 0 in split
+    // order: the split-K residual epilogue's arithmetic
+    // (splits are loaded PG at a time, every load of a group issued before
+    // the first add)
+    constexpr int PG = 4;
+    const float* pr = a.parts + static_cast<int64_t>(r) * a.ld_part;
+    float t[NV][4] = {};
+    for (int s0 = 0; s0 < a.n_parts; s0 += PG) {
+      f32x4_t p[PG][NV];
+#pragma unroll
+      for (int u = 0; u < PG; ++u)
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int c = lane + 64 * i;
+          p[u][i] = (s0 + u < a.n_parts && (FULL || c < nch))
+                        ? *reinterpret_cast<const f32x4_t*>(pr + (s0 + u) * a.part_stride + 4 * c)
+                        : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+      for (int u = 0; u < PG; ++u)
+        if (s0 + u < a.n_parts)
+#pragma unroll
+          for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t[i][k] += p[u][i][k];
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      if (!FULL && c >= nch) continue;
+      if (a.part_bias) {
+        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(a.part_bias + 4 * c);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[i][k] += b[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[i][k] += t[i][k];
+    }
+  }
   if constexpr (kRes) {
 #pragma unroll
     for (int i = 0; i < NV; ++i)
@@ -384,7 +431,13 @@ void launch_ln(const LnArgs& a, hipStream_t st) {
                    a.ld_y % 4 == 0 && al(a.in, a.in_dtype) && al(a.resid, a.resid_dtype) &&
                    al(a.xio, DT_F32) && al(a.x_out, DT_F32) && al(a.y_out, a.y_dtype) &&
                    al(a.w, DT_F32) && al(a.b, DT_F32);
-  if (vec && a.resid == nullptr) {
+  if (a.n_parts > 0) {
+    require(vec && a.resid == nullptr && a.in_dtype == DT_F32 && a.ids == nullptr && a.xio &&
+                a.parts && al(a.parts, DT_F32) && a.part_stride % 4 == 0 && a.ld_part % 4 == 0 &&
+                al(a.part_bias, DT_F32),
+            "layer_norm: split-K partials need fp32 vector rows written back to xio");
+    ln_vec_dispatch<float, PartsRes>(a, st);
+  } else if (vec && a.resid == nullptr) {
     a.in_dtype == DT_BF16 ? ln_vec_dispatch<bf16_t, NoRes>(a, st)
                           : ln_vec_dispatch<float, NoRes>(a, st);
   } else if (vec && a.in_dtype == DT_F32) {

@@ -57,10 +57,19 @@ struct GemmArgs {
   int n_w = 0;      // rows of W (= N, or 2F for GEGLU)
 };
 void launch_gemm(const GemmArgs& g, hipStream_t st);
+// Short batches (M <= 256) of a residual GEMM (EPI_RESID, bf16 MFMA path):
+// launches only the split-K product into g.partial and returns the number of
+// splits S >= 2; the caller then adds the splits with the layer norm that
+// reads X next (LnArgs::parts).  Returns 0, having launched nothing, when the
+// split-K path does not apply.
+int launch_gemm_resid_partials(const GemmArgs& g, hipStream_t st);
 
 // Row LayerNorm over [M, D] rows (src/tensor.cpp:54-79 semantics).
 //   input row r = in[(ids ? ids[r] : r) * ld_in]
 //   if resid: x = in_row + resid_row, written back to xio (fp32)
+//   if n_parts: x = in_row + (sum of the n_parts split-K partial rows, in
+//     split order, + part_bias), written back to xio (fp32): the residual
+//     epilogue of a split-K GEMM, bit for bit
 //   y = normalize ? LN(x) * w (+ b) : x
 //   x_out (fp32, optional) and y_out (y_dtype, optional) receive y.
 struct LnArgs {
@@ -71,6 +80,10 @@ struct LnArgs {
   const void* resid = nullptr;  // optional residual added first (resid_dtype)
   int resid_dtype = DT_BF16;
   float* xio = nullptr;  // where x = in + resid is written back (fp32 rows, ld_in)
+  const float* parts = nullptr;  // split-K partials: parts[s * part_stride + r * ld_part + c]
+  int n_parts = 0;
+  int64_t part_stride = 0, ld_part = 0;
+  const float* part_bias = nullptr;
   bool normalize = true;
   const float* w = nullptr;
   const float* b = nullptr;
