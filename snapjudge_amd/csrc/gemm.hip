@@ -1350,7 +1350,10 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
                     (g.epi != EPI_GEGLU || g.N % 64 == 0);
   if (g.epi == EPI_ROPE && !mfma)
     require(gBN % g.head_dim == 0, "gemm: ROPE epilogue needs head_dim dividing 64");
-  if (mfma && g.partial && g.M <= 256 && launch_splitk(g, st)) return;
+  // split-K only for the residual epilogue: its few output tiles (N = D)
+  // leave most CUs idle otherwise; the wider products (QKV, GEGLU) have
+  // enough tiles, and a second epilogue kernel costs more than it saves
+  if (mfma && g.partial && g.M <= 256 && g.epi == EPI_RESID && launch_splitk(g, st)) return;
   if (mfma) {
     launch_mfma(g, st);
     check_launch("gemm_bf16_mfma");
