@@ -631,16 +631,21 @@ __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)
 // in the ring stage the unit's last K step has just consumed: cos rows at
 // row * 128, sin rows 32 KB on (64 KB).  Loaded with direct-to-LDS copies of
 // whole 128-byte table rows, so the epilogue's per-element table reads are
-// LDS reads instead of one global gather per (row, dim).  Every wave of the
-// workgroup takes part (loads and both barriers).
-__device__ __forceinline__ void rope_stage_lds(const GemmArgs& g, char* tab, int m0, int wave_s,
-                                               int lane) {
+// LDS reads instead of one global gather per (row, dim).  The unit's row
+// positions were copied to LDS (pos_lds, 256 ints) when its first K step
+// began; with more K steps the loop's own waits and barriers have made them
+// visible, with one (one_step) this function waits for them.  Every wave of
+// the workgroup takes part (loads and barriers).
+__device__ __forceinline__ void rope_stage_lds(const GemmArgs& g, char* tab, const int* pos_lds,
+                                               int wave_s, int lane, bool one_step) {
+  if (one_step) {
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+  }
   int p[2];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int m = min(m0 + 8 * (wave_s + 16 * k) + (lane >> 3), g.M - 1);
-    p[k] = min(max(g.pos[m], 0), g.rope_rows - 1);
-  }
+  for (int k = 0; k < 2; ++k)
+    p[k] = min(max(pos_lds[8 * (wave_s + 16 * k) + (lane >> 3)], 0), g.rope_rows - 1);
   __builtin_amdgcn_s_barrier();  // every wave is done with the stage's operands
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -881,6 +886,18 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
         for (int t = 0; t < 8; ++t) bw[1][j][t] = static_cast<__bf16>(0.f);
       }
     }
+    const int m0 = tm * BM + (th < 0 ? 0 : (BM / 2) * th);
+    // RoPE units: positions of the unit's 256 rows to LDS (waves 0-3, 64 rows
+    // each), copied during the first K step and read at the unit's end
+    int* pos_lds = reinterpret_cast<int*>(dsmem + NS * TT::STAGE_BYTES);
+    auto copy_pos = [&]() {
+      if constexpr (kRopeLds) {
+        if (wave_s < 4 && tn * BN < 2 * g.rope_dim)
+          __builtin_amdgcn_global_load_lds(g.pos + min(m0 + 64 * wave_s + lane, g.M - 1),
+                                           (__attribute__((address_space(3))) void*)(pos_lds + 64 * wave_s),
+                                           4, 0, 0);
+      }
+    };
     auto kloop = [&](auto busy) {
       for (int kt = 0; kt < nk; ++kt, ++q) {
         // this wave's loads of stage q have landed once at most the younger
@@ -892,6 +909,7 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
         if (q + NS - 1 < total) issue_next((q + NS - 1) % NS);
+        if (kt == 0) copy_pos();
         if constexpr (!decltype(busy)::value) continue;
         const char* sb = dsmem + (q % NS) * TT::STAGE_BYTES;
         // operand reads of step 0 go out first; the previous stage's last K
@@ -921,13 +939,12 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
       }
       if constexpr (decltype(busy)::value) mma(KS - 1);
     };
-    const int m0 = tm * BM + (th < 0 ? 0 : (BM / 2) * th);
     const char* rope_tab = nullptr;
     auto stage_tables = [&]() {
       if constexpr (kRopeLds) {
         if (tn * BN < 2 * g.rope_dim) {  // uniform: the tile has rotated columns
           char* tab = dsmem + ((q + NS - 1) % NS) * TT::STAGE_BYTES;  // stage of the last K step
-          rope_stage_lds(g, tab, m0, wave_s, lane);
+          rope_stage_lds(g, tab, pos_lds, wave_s, lane, nk == 1);
           rope_tab = tab;
         }
       }
@@ -991,7 +1008,8 @@ int num_cus() {
 
 template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8, int EPI, typename OutT>
 void launch_pers_kernel(const GemmArgs& g, hipStream_t st) {
-  constexpr int lds = NS * PTile<BM, BN, WGM, WGN, NS, BK, W8>::STAGE_BYTES;
+  // (+ 1 KB of row positions for the RoPE epilogue)
+  constexpr int lds = NS * PTile<BM, BN, WGM, WGN, NS, BK, W8>::STAGE_BYTES + (EPI == EPI_ROPE ? 1024 : 0);
   auto kern = gemm_bf16_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI, OutT>;
   static bool attr_set = false;
   if (!attr_set) {
