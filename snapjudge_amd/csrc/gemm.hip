@@ -765,14 +765,13 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
   // ld_n), half ld_h) and K step ld_kt.
   int ld_kt = 0, ld_u = 0, ld_m, ld_n, ld_h;
   unit(0, ld_m, ld_n, ld_h);
-  // Per-lane source rows of the load tile, recomputed only when the cursor
-  // enters a new tile; each stage then adds its K offset.  The LDS target of
-  // each load instruction is wave-uniform and kept in scalar registers.
+  // Load addresses: a wave-uniform base (the operand's start plus the K
+  // step's byte offset, in scalar registers) plus a per-lane 32-bit byte
+  // offset of the source row and chunk, recomputed only when the cursor
+  // enters a new unit (the launcher checks that both operands span less than
+  // 4 GiB).  The LDS target of each load instruction is wave-uniform too.
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  const char* src[G];
-  int kbytes[G];  // bytes per K step of the group's operand
-#pragma unroll
-  for (int i = 0; i < G; ++i) kbytes[i] = wave_s + NW * i < TT::GA ? BK * 2 : RBW;
+  uint32_t voff[G];
   auto set_src = [&]() {
 #pragma unroll
     for (int i = 0; i < G; ++i) {
@@ -782,21 +781,26 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
         const int chunk = (lane % TT::CPRA) ^ TT::swz(RBA, row);
         // a half unit stages its BM/2 rows twice (the copy is never read)
         const int arow = ld_h < 0 ? row : (row & (BM / 2 - 1)) + (BM / 2) * ld_h;
-        src[i] = A + static_cast<int64_t>(min(ld_m * BM + arow, g.M - 1)) * g.lda * 2 + chunk * 16;
+        voff[i] = static_cast<uint32_t>(min(ld_m * BM + arow, g.M - 1)) * static_cast<uint32_t>(g.lda * 2) +
+                  chunk * 16;
       } else {
         const int row = TT::RPIW * (gi - TT::GA) + lane / TT::CPRW;
         const int chunk = (lane % TT::CPRW) ^ TT::swz(RBW, row);
-        src[i] = W + mfma_w_row<BN, TT::WN, EPI>(g, ld_n, row) * g.ldw * (W8 ? 1 : 2) +
-                 chunk * 16;
+        voff[i] = static_cast<uint32_t>(mfma_w_row<BN, TT::WN, EPI>(g, ld_n, row)) *
+                      static_cast<uint32_t>(g.ldw * (W8 ? 1 : 2)) +
+                  chunk * 16;
       }
     }
   };
   set_src();
   auto issue_next = [&](int buf) {
     char* base = dsmem + buf * TT::STAGE_BYTES + wave_s * 1024;
+    const char* a_k = A + ld_kt * (BK * 2);
+    const char* w_k = W + ld_kt * RBW;
 #pragma unroll
     for (int i = 0; i < G; ++i)
-      load_lds16(static_cast<const void*>(src[i] + ld_kt * kbytes[i]), base + NW * i * 1024);
+      load_lds16(static_cast<const void*>((wave_s + NW * i < TT::GA ? a_k : w_k) + voff[i]),
+                 base + NW * i * 1024);
     if (++ld_kt == nk) {  // next unit of the list
       ld_kt = 0;
       if (++ld_u < my_units) {
@@ -1103,10 +1107,15 @@ void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
 // of 128 x 64 (one workgroup per CU, 256 VGPRs per wave)
 #define SJH_GEMM_PERS_FP8 256, 256, 2, 4, 3, 64
 
-// The persistent kernel's epilogues write 8- and 16-byte vectors.
+// The persistent kernel's epilogues write 8- and 16-byte vectors, and its
+// loads address each operand by 32-bit byte offsets.
 bool pers_ok(const GemmArgs& g) {
+  const int64_t w_rows = g.epi == EPI_GEGLU ? 2 * static_cast<int64_t>(g.N) : g.N;
+  const int64_t w_bytes = g.w_dtype == DT_FP8 ? 1 : 2;
   return g.N % 4 == 0 && g.ldo % 4 == 0 && g.ldx % 4 == 0 && aligned16(g.out) &&
-         aligned16(g.X) && aligned16(g.bias) && aligned16(g.rope_cos) && aligned16(g.rope_sin);
+         aligned16(g.X) && aligned16(g.bias) && aligned16(g.rope_cos) && aligned16(g.rope_sin) &&
+         static_cast<int64_t>(g.M) * g.lda * 2 < (int64_t{1} << 32) &&
+         w_rows * g.ldw * w_bytes < (int64_t{1} << 32);
 }
 
 void launch_mfma(const GemmArgs& g, hipStream_t st) {
@@ -1355,7 +1364,7 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
     require(g.K % 64 == 0 && g.lda % 8 == 0 && g.ldw % 16 == 0 && aligned16(g.A) &&
                 aligned16(g.W),
             "gemm: fp8 weights need K % 64 == 0 and 16-byte aligned rows");
-    require(pers_ok(g), "gemm: fp8 weights need N % 4 == 0 and 16-byte aligned outputs");
+    require(pers_ok(g), "gemm: fp8 weights need N % 4 == 0, 16-byte aligned outputs and operands under 4 GiB");
     require(g.epi != EPI_ROPE || g.head_dim == 64, "gemm: fp8 RoPE epilogue needs head_dim 64");
     launch_pers<SJH_GEMM_PERS_FP8, true>(g, st);
     check_launch("gemm_fp8w");
