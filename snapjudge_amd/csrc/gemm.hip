@@ -642,16 +642,18 @@ __device__ __forceinline__ void rope_stage_lds(const GemmArgs& g, char* tab, con
     wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
   }
-  int p[2];
+  // byte offsets into the tables (under 4 GiB, checked by the launcher) over
+  // the tables' uniform bases
+  uint32_t off[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k)
-    p[k] = min(max(pos_lds[8 * (wave_s + 16 * k) + (lane >> 3)], 0), g.rope_rows - 1);
+    off[k] = static_cast<uint32_t>(min(max(pos_lds[8 * (wave_s + 16 * k) + (lane >> 3)], 0), g.rope_rows - 1)) * 128u +
+             (lane & 7) * 16;
   __builtin_amdgcn_s_barrier();  // every wave is done with the stage's operands
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float* t = (i >> 1) ? g.rope_sin : g.rope_cos;
-    load_lds16(t + static_cast<int64_t>(p[i & 1]) * 32 + (lane & 7) * 4,
-               tab + (i >> 1) * 32768 + (wave_s + 16 * (i & 1)) * 1024);
+    const char* t = reinterpret_cast<const char*>((i >> 1) ? g.rope_sin : g.rope_cos);
+    load_lds16(t + off[i & 1], tab + (i >> 1) * 32768 + (wave_s + 16 * (i & 1)) * 1024);
   }
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
@@ -897,7 +899,7 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
     auto copy_pos = [&]() {
       if constexpr (kRopeLds) {
         if (wave_s < 4 && tn * BN < 2 * g.rope_dim)
-          __builtin_amdgcn_global_load_lds(g.pos + min(m0 + 64 * wave_s + lane, g.M - 1),
+          __builtin_amdgcn_global_load_lds(g.pos + min(m0 + 64 * wave_s + lane_id_here(), g.M - 1),
                                            (__attribute__((address_space(3))) void*)(pos_lds + 64 * wave_s),
                                            4, 0, 0);
       }
@@ -948,7 +950,7 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
       if constexpr (kRopeLds) {
         if (tn * BN < 2 * g.rope_dim) {  // uniform: the tile has rotated columns
           char* tab = dsmem + ((q + NS - 1) % NS) * TT::STAGE_BYTES;  // stage of the last K step
-          rope_stage_lds(g, tab, pos_lds, wave_s, lane, nk == 1);
+          rope_stage_lds(g, tab, pos_lds, wave_s, lane_id_here(), nk == 1);
           rope_tab = tab;
         }
       }
@@ -960,6 +962,10 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
     }
     kloop(std::true_type{});
     stage_tables();
+    // the epilogue's lane and wave indices, recomputed after the K loop
+    // rather than held through it
+    const int lane_e = lane_id_here(), l32e = lane_e & 31, hbe = lane_e >> 5;
+    const int wme = wm_s, wne = wave_s % WGN;
     if constexpr (W8) {
       // row n of W stands for code * w_scale[n]: scale the accumulators
       if constexpr (kSwap) {
@@ -971,7 +977,7 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
         for (int j = 0; j < TJ; ++j)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int64_t r0 = min(mfma_w_row<BN, TT::WN, EPI>(g, tn, wn * TT::WN + j * 32 + 8 * q + 4 * hb),
+            const int64_t r0 = min(mfma_w_row<BN, TT::WN, EPI>(g, tn, wne * TT::WN + j * 32 + 8 * q + 4 * hbe),
                                    nrows - 4);
             const f32x4_t sc = *reinterpret_cast<const f32x4_t*>(g.w_scale + r0);
 #pragma unroll
@@ -982,7 +988,7 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
       } else {
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-          const float sc = g.w_scale[mfma_w_row<BN, TT::WN, EPI>(g, tn, wn * TT::WN + j * 32 + l32)];
+          const float sc = g.w_scale[mfma_w_row<BN, TT::WN, EPI>(g, tn, wne * TT::WN + j * 32 + l32e)];
 #pragma unroll
           for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -991,9 +997,9 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
       }
     }
     if constexpr (kSwap)
-      pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wm, wn, l32, hb);
+      pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wme, wne, l32e, hbe);
     else
-      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wm, wn, l32, hb,
+      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wme, wne, l32e, hbe,
                                                                rope_tab);
   }
 }
@@ -1115,7 +1121,8 @@ bool pers_ok(const GemmArgs& g) {
   return g.N % 4 == 0 && g.ldo % 4 == 0 && g.ldx % 4 == 0 && aligned16(g.out) &&
          aligned16(g.X) && aligned16(g.bias) && aligned16(g.rope_cos) && aligned16(g.rope_sin) &&
          static_cast<int64_t>(g.M) * g.lda * 2 < (int64_t{1} << 32) &&
-         w_rows * g.ldw * w_bytes < (int64_t{1} << 32);
+         w_rows * g.ldw * w_bytes < (int64_t{1} << 32) &&
+         (g.epi != EPI_ROPE || static_cast<int64_t>(g.rope_rows) * 128 < (int64_t{1} << 32));
 }
 
 void launch_mfma(const GemmArgs& g, hipStream_t st) {

@@ -104,6 +104,16 @@ __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
 
+// The lane's index in its wavefront, computed where it is used: the asm
+// cannot be hoisted or merged with an earlier copy, so a kernel near its
+// register limit recomputes the value (two VALU ops) instead of keeping it
+// live, or spilling it, across a long loop.
+__device__ __forceinline__ int lane_id_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // Direct-to-LDS 16-byte load: lane l's 16 bytes from src land at
 // lds_base + 16 * l (lds_base must be the same for the whole wave).
 __device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
