@@ -146,7 +146,9 @@ __device__ __forceinline__ void consume(const T& v) {
 }
 
 // Epilogue on the accumulators in registers (see the comment above).
-template <int BM, int BN, int WM, int WN, int TI, int TJ, int EPI, typename OutT>
+// TAB_LDS: the RoPE table rows of the tile are staged in LDS at rope_tab
+// (given whenever the tile has rotated columns).
+template <int BM, int BN, int WM, int WN, int TI, int TJ, int EPI, typename OutT, bool TAB_LDS = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int m0,
                                               int tile_n, int wm, int wn, int l32, int hb,
                                               const char* rope_tab = nullptr) {
@@ -170,106 +172,132 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
   } else if constexpr (EPI == EPI_RESID) {
     // X += acc (+ bias).  The X reads of a group of RG rows are all issued
     // before the first add, so a group costs one memory round trip rather
-    // than one per element (rows past M read row M - 1 and store nothing).
+    // than one per element.  Addresses are the wave's uniform corner plus one
+    // 32-bit byte offset per access; elements past M or N are skipped.
     constexpr int RG = 4;
-    const int c0 = tile_n * BN + wn * WN + l32;
+    const int c0 = tile_n * BN + wn * WN;
+    const int rw = m0 + wm * WM;  // the wave's first row
+    const char* xw = reinterpret_cast<const char*>(g.X + static_cast<int64_t>(rw) * g.ldx + c0);
+    const uint32_t ld4 = static_cast<uint32_t>(g.ldx) * 4u;
+    const uint32_t lo = 4 * hb * ld4 + l32 * 4;
+    const bool rfull = rw + WM <= g.M, cfull = c0 + WN <= g.N;  // uniform
     float bv[TJ];
-    int cc[TJ];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      bv[j] = (g.bias && c0 + j * 32 < g.N) ? g.bias[c0 + j * 32] : 0.f;
-      cc[j] = min(c0 + j * 32, g.N - 1);
-      consume(bv[j]);
-    }
+    for (int j = 0; j < TJ; ++j) bv[j] = g.bias ? g.bias[min(c0 + j * 32 + l32, g.N - 1)] : 0.f;
+    auto body = [&](auto checked) {  // checked: the wave's rows or columns run past M or N
+      auto in = [&](int r, int j) {
+        if constexpr (decltype(checked)::value)
+          return rw + r + 4 * hb < g.M && c0 + j * 32 + l32 < g.N;
+        return true;
+      };
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int e0 = 0; e0 < 16; e0 += RG) {
-        float xv[RG][TJ];
+        for (int e0 = 0; e0 < 16; e0 += RG) {
+          float xv[RG][TJ];
 #pragma unroll
-        for (int e = 0; e < RG; ++e) {
-          const int m = min(row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3), g.M - 1);
-          const float* xrow = g.X + static_cast<int64_t>(m) * g.ldx;
+          for (int e = 0; e < RG; ++e) {
+            const int r = i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3);
+            const char* xr = xw + static_cast<uint32_t>(r * ld4 + lo);
 #pragma unroll
-          for (int j = 0; j < TJ; ++j) xv[e][j] = xrow[cc[j]];
+            for (int j = 0; j < TJ; ++j)
+              xv[e][j] = in(r, j) ? *reinterpret_cast<const float*>(xr + j * 128) : 0.f;
+          }
+#pragma unroll
+          for (int e = 0; e < RG; ++e) {
+            const int r = i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3);
+            char* xr = const_cast<char*>(xw) + static_cast<uint32_t>(r * ld4 + lo);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+              if (in(r, j)) *reinterpret_cast<float*>(xr + j * 128) = xv[e][j] + (acc[i][j][e0 + e] + bv[j]);
+          }
         }
-#pragma unroll
-        for (int e = 0; e < RG; ++e)
-#pragma unroll
-          for (int j = 0; j < TJ; ++j) consume(xv[e][j]);
-#pragma unroll
-        for (int e = 0; e < RG; ++e) {
-          const int m = row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3);
-          if (m >= g.M) continue;
-          float* xrow = g.X + static_cast<int64_t>(m) * g.ldx;
-#pragma unroll
-          for (int j = 0; j < TJ; ++j)
-            if (c0 + j * 32 < g.N) xrow[c0 + j * 32] = xv[e][j] + (acc[i][j][e0 + e] + bv[j]);
-        }
-      }
+    };
+    if (rfull && cfull)
+      body(std::false_type{});
+    else
+      body(std::true_type{});
   } else if constexpr (EPI == EPI_ROPE) {
     // head_dim 64 (checked by the launcher): block j holds dims [0, 32) of a
     // head when j is even and dims [32, 64) when odd; its partner is j ^ 1.
-    // Positions and table entries of a group of RG rows are fetched together
-    // (two memory round trips per group, not two per row).
+    // Table entries of a group of RG rows are fetched together: from the
+    // unit's table rows in LDS (rope_tab) or, without them, gathered through
+    // the positions (two memory round trips per group, not two per row).
+    // Addresses are the wave's uniform corner plus one 32-bit byte offset per
+    // access; elements past M or N are skipped.
     static_assert(TJ % 2 == 0, "RoPE pairs need an even number of column blocks");
     constexpr int RG = 8;
-    OutT* out = static_cast<OutT*>(g.out);
+    constexpr int EB = sizeof(OutT);
     const int c0 = tile_n * BN + wn * WN;
+    const int rw = m0 + wm * WM;  // the wave's first row
+    const char* ow = reinterpret_cast<const char*>(static_cast<OutT*>(g.out) + static_cast<int64_t>(rw) * g.ldo + c0);
+    const uint32_t ldb = static_cast<uint32_t>(g.ldo) * EB;
+    const uint32_t lo = 4 * hb * ldb + l32 * EB;
+    const bool rfull = rw + WM <= g.M, cfull = c0 + WN <= g.N;  // uniform
+    const bool wave_rot = c0 < 2 * g.rope_dim;  // rotated blocks come first in a row
+    auto body = [&](auto checked) {  // checked: the wave's rows or columns run past M or N
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int e0 = 0; e0 < 16; e0 += RG) {
-        float cs[RG], sn[RG];
-        if (rope_tab) {
-          // the unit's table rows, staged in LDS: cos at row * 128, sin 32 KB on
-          const int rl = row_base - m0 + i * 32;
+        for (int e0 = 0; e0 < 16; e0 += RG) {
+          float cs[RG], sn[RG];
+          if (wave_rot) {
+            if constexpr (TAB_LDS) {
+              // the unit's table rows: cos at row * 128, sin 32 KB on
+              typedef __attribute__((address_space(3))) const float lds_f32;
+              lds_f32* t = (lds_f32*)(rope_tab + (rw - m0 + 4 * hb + i * 32) * 128 + l32 * 4);
 #pragma unroll
-          for (int e = 0; e < RG; ++e) {
-            const char* t = rope_tab + (rl + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3)) * 128 + l32 * 4;
-            cs[e] = *reinterpret_cast<const float*>(t);
-            sn[e] = *reinterpret_cast<const float*>(t + 32768);
-          }
-        } else {
-          int p[RG];
+              for (int e = 0; e < RG; ++e) {
+                const int r = 8 * ((e0 + e) >> 2) + ((e0 + e) & 3);
+                cs[e] = t[r * 32];
+                sn[e] = t[r * 32 + 8192];
+              }
+            } else {
+              int p[RG];
 #pragma unroll
-          for (int e = 0; e < RG; ++e) {
-            const int m = min(row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3), g.M - 1);
-            p[e] = g.pos[m];
-          }
+              for (int e = 0; e < RG; ++e) {
+                const int m = min(rw + 4 * hb + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3), g.M - 1);
+                p[e] = g.pos[m];
+              }
 #pragma unroll
-          for (int e = 0; e < RG; ++e) {
-            const int64_t tb = static_cast<int64_t>(min(max(p[e], 0), g.rope_rows - 1)) * 32 + l32;
-            cs[e] = g.rope_cos[tb];
-            sn[e] = g.rope_sin[tb];
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < RG; ++e) {
-          consume(cs[e]);
-          consume(sn[e]);
-        }
-#pragma unroll
-        for (int e = 0; e < RG; ++e) {
-          const int m = row_base + i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3);
-          if (m >= g.M) continue;
-          OutT* orow = out + static_cast<int64_t>(m) * g.ldo;
-#pragma unroll
-          for (int j = 0; j < TJ; j += 2) {
-            const int col = c0 + j * 32 + l32;
-            if (col >= g.N) continue;
-            float x0 = acc[i][j][e0 + e], x1 = acc[i][j + 1][e0 + e];
-            if (c0 + j * 32 < 2 * g.rope_dim) {
-              const float r0 = rope_lo(x0, x1, cs[e], sn[e]);
-              const float r1 = rope_hi(x0, x1, cs[e], sn[e]);
-              x0 = r0;
-              x1 = r1;
+              for (int e = 0; e < RG; ++e) {
+                const int64_t tb = static_cast<int64_t>(min(max(p[e], 0), g.rope_rows - 1)) * 32 + l32;
+                cs[e] = g.rope_cos[tb];
+                sn[e] = g.rope_sin[tb];
+              }
             }
-            store_f32(orow + col, x0);
-            if (col + 32 < g.N) store_f32(orow + col + 32, x1);
+#pragma unroll
+            for (int e = 0; e < RG; ++e) {
+              consume(cs[e]);
+              consume(sn[e]);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < RG; ++e) {
+            const int r = i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3);
+            if (decltype(checked)::value && rw + r + 4 * hb >= g.M) continue;
+            char* orow = const_cast<char*>(ow) + static_cast<uint32_t>(r * ldb + lo);
+#pragma unroll
+            for (int j = 0; j < TJ; j += 2) {
+              const int col = c0 + j * 32 + l32;
+              if (decltype(checked)::value && col >= g.N) continue;
+              float x0 = acc[i][j][e0 + e], x1 = acc[i][j + 1][e0 + e];
+              if (wave_rot && c0 + j * 32 < 2 * g.rope_dim) {
+                const float r0 = rope_lo(x0, x1, cs[e], sn[e]);
+                const float r1 = rope_hi(x0, x1, cs[e], sn[e]);
+                x0 = r0;
+                x1 = r1;
+              }
+              store_f32(reinterpret_cast<OutT*>(orow + j * 32 * EB), x0);
+              if (!decltype(checked)::value || col + 32 < g.N) store_f32(reinterpret_cast<OutT*>(orow + (j + 1) * 32 * EB), x1);
+            }
           }
         }
-      }
+    };
+    if (rfull && cfull)
+      body(std::false_type{});
+    else
+      body(std::true_type{});
   } else {
     OutT* out = static_cast<OutT*>(g.out);
     const int c0 = tile_n * BN + wn * WN + l32;
@@ -627,21 +655,15 @@ __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)
   }
 }
 
-// RoPE tables of a persistent unit's 256 rows staged in LDS for its epilogue,
-// in the ring stage the unit's last K step has just consumed: cos rows at
-// row * 128, sin rows 32 KB on (64 KB).  Loaded with direct-to-LDS copies of
-// whole 128-byte table rows, so the epilogue's per-element table reads are
-// LDS reads instead of one global gather per (row, dim).  The unit's row
-// positions were copied to LDS (pos_lds, 256 ints) when its first K step
-// began; with more K steps the loop's own waits and barriers have made them
-// visible, with one (one_step) this function waits for them.  Every wave of
-// the workgroup takes part (loads and barriers).
-__device__ __forceinline__ void rope_stage_lds(const GemmArgs& g, char* tab, const int* pos_lds,
-                                               int wave_s, int lane, bool one_step) {
-  if (one_step) {
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
-  }
+// RoPE tables of a persistent unit's 256 rows staged in LDS for its epilogue:
+// cos rows at row * 128, sin rows 32 KB on (64 KB), copied with direct-to-LDS
+// loads of whole 128-byte table rows, so that the epilogue's per-element
+// table reads are LDS reads instead of one global gather per (row, dim).  The
+// row positions come from pos_lds (the unit's 256 positions, copied there
+// when its first K step began).  Each of the 16 waves copies 16 rows (four
+// load instructions); the caller provides the waits and barriers.
+__device__ __forceinline__ void rope_issue_tables(const GemmArgs& g, char* tab, const int* pos_lds,
+                                                  int wave_s, int lane) {
   // byte offsets into the tables (under 4 GiB, checked by the launcher) over
   // the tables' uniform bases
   uint32_t off[2];
@@ -649,14 +671,11 @@ __device__ __forceinline__ void rope_stage_lds(const GemmArgs& g, char* tab, con
   for (int k = 0; k < 2; ++k)
     off[k] = static_cast<uint32_t>(min(max(pos_lds[8 * (wave_s + 16 * k) + (lane >> 3)], 0), g.rope_rows - 1)) * 128u +
              (lane & 7) * 16;
-  __builtin_amdgcn_s_barrier();  // every wave is done with the stage's operands
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const char* t = reinterpret_cast<const char*>((i >> 1) ? g.rope_sin : g.rope_cos);
     load_lds16(t + off[i & 1], tab + (i >> 1) * 32768 + (wave_s + 16 * (i & 1)) * 1024);
   }
-  wait_vmcnt<0>();
-  __builtin_amdgcn_s_barrier();
 }
 
 // Ring geometry of the persistent kernel.  A rows are bf16; W rows are bf16,
@@ -865,6 +884,12 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
   // LDS reads issued by frag(s)
   auto nreads = [](int s) { return TI + (W8 ? ((s & 1) == 0 ? TJ : 0) : TJ); };
 
+  // Ring slot of stage q: (q + so) % NS.  A RoPE unit with rotated columns
+  // and at least two K steps copies its table rows during its last K step,
+  // into the slot that step leaves free (where the next unit's first stage
+  // would otherwise go); that stage goes instead into the slot the last step
+  // consumed, once every wave is done with it, so the slot order flips.
+  int so = 0;
   int q = 0;  // global stage counter (ring position)
   for (int r = 0; r < my_units; ++r) {
     int tm, tn, th;  // compute cursor: the unit whose stages are consumed
@@ -904,6 +929,8 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
                                            4, 0, 0);
       }
     };
+    // uniform: the unit's tile has rotated columns
+    const bool rot = kRopeLds && tn * BN < 2 * g.rope_dim;
     auto kloop = [&](auto busy) {
       for (int kt = 0; kt < nk; ++kt, ++q) {
         // this wave's loads of stage q have landed once at most the younger
@@ -914,10 +941,14 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
           wait_vmcnt<0>();
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
-        if (q + NS - 1 < total) issue_next((q + NS - 1) % NS);
+        if (rot && nk >= 2 && kt == nk - 1)
+          rope_issue_tables(g, dsmem + ((q + NS - 1 + so) % NS) * TT::STAGE_BYTES, pos_lds, wave_s,
+                            lane_id_here());
+        else if (q + NS - 1 < total)
+          issue_next((q + NS - 1 + so) % NS);
         if (kt == 0) copy_pos();
         if constexpr (!decltype(busy)::value) continue;
-        const char* sb = dsmem + (q % NS) * TT::STAGE_BYTES;
+        const char* sb = dsmem + ((q + so) % NS) * TT::STAGE_BYTES;
         // operand reads of step 0 go out first; the previous stage's last K
         // step (deferred past the barrier) covers their latency; then each
         // step's MFMAs interleave one-for-one with the reads of the next step
@@ -946,12 +977,35 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
       if constexpr (decltype(busy)::value) mma(KS - 1);
     };
     const char* rope_tab = nullptr;
-    auto stage_tables = [&]() {
+    auto stage_tables = [&]() {  // every wave takes part (loads and barriers)
       if constexpr (kRopeLds) {
-        if (tn * BN < 2 * g.rope_dim) {  // uniform: the tile has rotated columns
-          char* tab = dsmem + ((q + NS - 1) % NS) * TT::STAGE_BYTES;  // stage of the last K step
-          rope_stage_lds(g, tab, pos_lds, wave_s, lane_id_here(), nk == 1);
-          rope_tab = tab;
+        if (rot) {
+          static_assert(NS == 2, "the table slot is the ring's other slot");
+          const int last = (q - 1 + so) % NS;  // slot of the last K step
+          wait_lgkm0();
+          if (nk >= 2) {
+            // the tables are in flight into the other slot; the next unit's
+            // first stage takes the last step's slot once every wave is done
+            // with it, and its loads stay in flight through the epilogue
+            __builtin_amdgcn_s_barrier();
+            rope_tab = dsmem + (1 - last) * TT::STAGE_BYTES;
+            const bool more = q < total;
+            if (more) issue_next(last);
+            so ^= 1;
+            if (more)
+              wait_vmcnt<G>();
+            else
+              wait_vmcnt<0>();
+          } else {
+            // one K step: the positions copied when it began land first, then
+            // the tables go into the last step's slot
+            wait_vmcnt<0>();
+            __builtin_amdgcn_s_barrier();
+            rope_tab = dsmem + last * TT::STAGE_BYTES;
+            rope_issue_tables(g, const_cast<char*>(rope_tab), pos_lds, wave_s, lane_id_here());
+            wait_vmcnt<0>();
+          }
+          __builtin_amdgcn_s_barrier();  // every wave's table rows have landed
         }
       }
     };
@@ -999,7 +1053,7 @@ void gemm_bf16_pers_kernel(GemmArgs g) {
     if constexpr (kSwap)
       pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wme, wne, l32e, hbe);
     else
-      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wme, wne, l32e, hbe,
+      gemm_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT, kRopeLds>(g, acc, m0, tn, wme, wne, l32e, hbe,
                                                                rope_tab);
   }
 }
