@@ -174,7 +174,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
     // before the first add, so a group costs one memory round trip rather
     // than one per element.  Addresses are the wave's uniform corner plus one
     // 32-bit byte offset per access; elements past M or N are skipped.
-    constexpr int RG = 4;
+    constexpr int RG = 8;
     const int c0 = tile_n * BN + wn * WN;
     const int rw = m0 + wm * WM;  // the wave's first row
     const char* xw = reinterpret_cast<const char*>(g.X + static_cast<int64_t>(rw) * g.ldx + c0);
