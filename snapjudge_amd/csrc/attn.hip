@@ -73,15 +73,33 @@ __device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
 // different waves overlap.
 __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kNS * kStage];
-  const int b = a.seq_order ? a.seq_order[blockIdx.z] : static_cast<int>(blockIdx.z);
-  const int h = blockIdx.y;
-  const int qlen = a.q_len ? a.q_len[b] : a.uniform_L;
-  const int q0 = blockIdx.x * kQ;
+  // Workgroup -> (sequence, head, query block).  Hardware hands workgroup i
+  // to XCD i % 8.  The (sequence, head) pairs, in seq_order's order, go to the
+  // XCDs round-robin, and an XCD's workgroups take its pairs' query blocks in
+  // turn, so the blocks of one pair run on one XCD close together and share
+  // its L2 for the pair's K/V tiles.
+  const int nblk = (a.max_q + kQ - 1) / kQ;
+  const int xcd = blockIdx.x & 7, kx = blockIdx.x >> 3;
+  const int pair = xcd + 8 * (kx / nblk);
+  if (pair >= a.H * a.B) return;  // uniform over the workgroup
+  const int zs = pair / a.H, h = pair - zs * a.H;
+  int qlen, klen;
+  int64_t row0;
+  if (a.seq_meta) {
+    const int4 m = reinterpret_cast<const int4*>(a.seq_meta)[zs];
+    row0 = m.x;
+    qlen = m.y;
+    klen = m.z;
+  } else {
+    const int b = a.seq_order ? a.seq_order[zs] : zs;
+    qlen = a.q_len ? a.q_len[b] : a.uniform_L;
+    // keys never extend past the rows a sequence owns (a caller's k_len > L
+    // in the padded layout is clamped rather than read out of bounds)
+    klen = a.seq_start ? a.k_len[b] : max(0, min(a.k_len[b], a.uniform_L));
+    row0 = a.seq_start ? a.seq_start[b] : static_cast<int64_t>(b) * a.uniform_L;
+  }
+  const int q0 = (kx % nblk) * kQ;
   if (q0 >= qlen) return;  // uniform over the workgroup
-  // keys never extend past the rows a sequence owns (a caller's k_len > L in
-  // the padded layout is clamped rather than read out of bounds)
-  const int klen = a.seq_start ? a.k_len[b] : max(0, min(a.k_len[b], a.uniform_L));
-  const int64_t row0 = a.seq_start ? a.seq_start[b] : static_cast<int64_t>(b) * a.uniform_L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hb = lane >> 5;
 
@@ -420,12 +438,18 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
               a.ld_o >= a.H * a.Dh,
           "attention: row stride < H*Dh");
   require(a.window >= 0, "attention: negative window");
+  require(!a.seq_meta || (a.seq_start && a.q_len && (reinterpret_cast<uintptr_t>(a.seq_meta) & 15u) == 0),
+          "attention: seq_meta needs the varlen layout and 16-byte alignment");
   const bool mfma = a.dtype == DT_BF16 && a.Dh == 64 && a.ld_q % 8 == 0 && a.ld_k % 8 == 0 &&
                     a.ld_v % 8 == 0 && a.ld_o % 4 == 0 && aligned16(a.q) && aligned16(a.k) &&
                     aligned16(a.v) && (reinterpret_cast<uintptr_t>(a.o) & 7u) == 0;
   if (mfma) {
-    dim3 grid((a.max_q + kQ - 1) / kQ, a.H, a.B), block(256);
-    attn_bf16_mfma_kernel<<<grid, block, 0, st>>>(a);
+    // one workgroup per (sequence, head, query block), the pairs padded to a
+    // multiple of the 8 XCDs (see the kernel's mapping)
+    const int64_t pairs8 = (static_cast<int64_t>(a.H) * a.B + 7) / 8 * 8;
+    const int64_t nwg = pairs8 * ((a.max_q + kQ - 1) / kQ);
+    require(nwg < (int64_t{1} << 31), "attention: too many workgroups");
+    attn_bf16_mfma_kernel<<<dim3(static_cast<unsigned>(nwg)), dim3(256), 0, st>>>(a);
     check_launch("attn_bf16_mfma");
     return;
   }

@@ -98,6 +98,12 @@ void quantize_fp8_rows(const float* w, size_t rows, size_t cols, uint8_t* q, flo
 }
 
 namespace {
+// Per-batch sequence table on the device: five arrays of B ints (seq_start,
+// q_len, k_len, qtype, order), padded to a 16-byte boundary, then B
+// {seq_start, q_len, k_len, 0} quadruples in attention order.
+size_t seqinfo_meta_off(int B) { return (static_cast<size_t>(5) * B + 3) / 4 * 4; }
+size_t seqinfo_ints(int B) { return seqinfo_meta_off(B) + static_cast<size_t>(4) * B; }
+
 
 uint16_t bf16_rne(float f) {
   uint32_t u;
@@ -381,7 +387,7 @@ void Engine::ensure_workspace(int T, int B) {
   ids_.ensure(t * 4);
   tok_pos_.ensure(t * 4);
   tok_seq_.ensure(t * 4);
-  seqinfo_.ensure(static_cast<size_t>(5) * std::max(nB, 1) * 4);
+  seqinfo_.ensure(seqinfo_ints(std::max(nB, 1)) * 4);
   X_.ensure(t * D * 4);
   Y_.ensure(t * D * as);
   QKV_.ensure(t * 3 * D * as);
@@ -403,8 +409,10 @@ void Engine::ensure_workspace(int T, int B) {
 
 void Engine::upload_batch(const BatchPlan& p, const int32_t* h_ids, const int32_t* h_qtype,
                           hipStream_t st) {
-  // pinned staging: [seq_start | q_len | k_len | qtype | order] then the token ids
-  const size_t nsi = static_cast<size_t>(5) * p.B;
+  // pinned staging: [seq_start | q_len | k_len | qtype | order | pad to 16 B |
+  // meta] then the token ids; meta[z] = {seq_start, q_len, k_len, 0} of the
+  // z-th sequence in attention order, one 16-byte load for a workgroup
+  const size_t nsi = seqinfo_ints(p.B);
   h_stage_.ensure((nsi + (h_ids ? p.T : 0)) * 4);
   int32_t* s = h_stage_.as<int32_t>();
   std::memcpy(s, p.seq_start.data(), p.B * 4);
@@ -412,6 +420,14 @@ void Engine::upload_batch(const BatchPlan& p, const int32_t* h_ids, const int32_
   std::memcpy(s + 2 * p.B, p.k_len.data(), p.B * 4);
   for (int b = 0; b < p.B; ++b) s[3 * p.B + b] = h_qtype ? h_qtype[b] : 0;
   std::memcpy(s + 4 * p.B, p.order.data(), p.B * 4);
+  int32_t* meta = s + seqinfo_meta_off(p.B);
+  for (int z = 0; z < p.B; ++z) {
+    const size_t b = static_cast<size_t>(p.order[static_cast<size_t>(z)]);
+    meta[4 * z + 0] = p.seq_start[b];
+    meta[4 * z + 1] = p.q_len[b];
+    meta[4 * z + 2] = p.k_len[b];
+    meta[4 * z + 3] = 0;
+  }
   hip_check(hipMemcpyAsync(seqinfo_.get(), s, nsi * 4, hipMemcpyHostToDevice, st), "upload seqinfo");
   if (h_ids) {
     std::memcpy(s + nsi, h_ids, static_cast<size_t>(p.T) * 4);
@@ -629,6 +645,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       a.q_len = q_len;
       a.k_len = k_len;
       a.seq_order = si + 4 * p.B;
+      a.seq_meta = si + seqinfo_meta_off(p.B);
       a.B = p.B;
       a.H = H_;
       a.Dh = Dh_;
@@ -785,6 +802,7 @@ void Engine::enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st) {
     at.q_len = si + p.B;
     at.k_len = si + 2 * p.B;
     at.seq_order = si + 4 * p.B;
+    at.seq_meta = si + seqinfo_meta_off(p.B);
     at.B = p.B;
     at.H = H_;
     at.Dh = Dh_;

@@ -116,6 +116,9 @@ struct AttnArgs {
   const int* q_len = nullptr;
   const int* k_len = nullptr;
   const int* seq_order = nullptr;  // optional: workgroup z handles sequence seq_order[z]
+  // optional, 16-byte aligned: seq_meta[4z .. 4z+3] = {seq_start, q_len,
+  // k_len, 0} of the sequence seq_order[z] (one load instead of a chain)
+  const int* seq_meta = nullptr;
   int B = 0, H = 0, Dh = 0;
   int max_q = 0;  // upper bound of q_len over the batch (grid size)
   int uniform_L = 0;
