@@ -315,6 +315,44 @@ def test_gemm_persistent_half_units(orc, kind):
         assert rel_err(host(O), want) < 8e-3
 
 
+@pytest.mark.parametrize("kind", ["store", "resid", "geglu", "rope"])
+def test_gemm_persistent_ragged_columns(orc, kind):
+    # persistent kernel (M >= 4096) whose last row tile runs past M and whose
+    # last column tile runs past N: the epilogues' bounds-checked instantiation
+    # next to the bounds-free one; three K steps, so RoPE tables are copied
+    # during the last K step
+    M, K, H, Dh, L = 4500, 192, 5, 64, 700
+    n = {"store": 320, "resid": 320, "geglu": 320, "rope": 3 * H * Dh}[kind]
+    nw = 2 * n if kind == "geglu" else n
+    print(f"persistent ragged columns: {kind} M={M} N={n} K={K}", flush=True)
+    rng = np.random.default_rng(91)
+    a, w, b = rnd(rng, (M, K)), rnd(rng, (nw, K), 0.1), rnd(rng, n)
+    A, W = dev(a, torch.bfloat16), dev(w, torch.bfloat16)
+    if kind == "store":
+        Bv = dev(b, torch.float32)
+        O = torch.empty((M, n), dtype=torch.bfloat16, device="cuda")
+        call(sj.lib().sjh_gemm, P(A), P(W), P(Bv), P(O), M, n, K, 2, BF, stream())
+        assert rel_err(host(O), orc.gemm_nt(a, w, b, 2)) < 8e-3
+    elif kind == "resid":
+        x0 = rng.standard_normal((M, n)).astype(np.float32)
+        X = dev(x0, torch.float32)
+        call(sj.lib().sjh_gemm_residual, P(A), P(W), P(X), M, n, K, BF, stream())
+        assert float(np.abs(host(X) - (x0 + orc.gemm_nt(a, w))).max()) < 2e-4
+    elif kind == "geglu":
+        O = torch.empty((M, n), dtype=torch.bfloat16, device="cuda")
+        call(sj.lib().sjh_gemm_geglu, P(A), P(W), P(O), M, n, K, BF, stream())
+        assert rel_err(host(O), orc.gemm_geglu(a, w)) < 8e-3
+    else:
+        c, s = orc.rope_table(160000.0, L, Dh)
+        Ct, St = dev(c, torch.float32), dev(s, torch.float32)
+        Pt = torch.from_numpy((np.arange(M) % L).astype(np.int32)).cuda()
+        O = torch.empty((M, n), dtype=torch.bfloat16, device="cuda")
+        call(sj.lib().sjh_gemm_qkv_rope, P(A), P(W), P(O), P(Pt), P(Ct), P(St), L, M, H, Dh, K,
+             BF, stream())
+        want = orc.rope_inplace(orc.gemm_nt(a, w), c, s, L, H, Dh)
+        assert rel_err(host(O), want) < 8e-3
+
+
 def test_gemm_tile_shape_invariance():
     # the tile shape is chosen from M; a row's result must not depend on it
     # (bit-identical for every epilogue)
