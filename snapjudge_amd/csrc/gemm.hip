@@ -1158,8 +1158,9 @@ void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
 // Tile shapes by row count (BM, BN, wave grid, ring stages, K step): 256x256
 // with 16 waves of 64x64 (4 waves per SIMD hide the LDS and MFMA latencies)
 // for the throughput shapes; 128x128 with 4 waves for mid-size batches;
-// 64x128 with 4 waves of 32x64 for short ones (batch-1 latency), where more
-// workgroups are needed to spread the weight reads over the CUs.
+// 64x64 with 2 waves of 32x64 and a 4-stage ring for short ones (batch-1
+// latency): more workgroups spread the weight reads over the CUs, and three
+// stages in flight cover the load latency that bounds such a short loop.
 #ifndef SJH_GEMM_PERS
 #define SJH_GEMM_PERS 256, 256, 4, 4, 2, 64
 #endif
@@ -1187,7 +1188,7 @@ void launch_mfma(const GemmArgs& g, hipStream_t st) {
   else if (g.M >= 1024)
     launch_mfma_epi<SJH_GEMM_MID>(g, st);
   else
-    launch_mfma_epi<64, 128, 2, 2, 2, 64>(g, st);
+    launch_mfma_epi<64, 64, 2, 1, 4, 64>(g, st);
 }
 
 // ------------------------------------------------------------------ split-K
