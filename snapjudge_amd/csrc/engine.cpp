@@ -1021,9 +1021,11 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     run_device_maybe_graph(p, ids_.as<int32_t>(), X_.as<float>(), true, st);
   }
 
-  // ---- scorer (src/model.cpp:461-487) on device: gather marker rows and CLS rows
+  // ---- scorer (src/model.cpp:461-487) and act head (:489-535), all on the
+  // device: gather the marker rows and the [CLS] rows, then only the logits
+  // and the act probabilities come back
   const int nmk = B * K, nrow = nmk + B;
-  std::vector<int32_t> idx(static_cast<size_t>(nrow));
+  std::vector<int32_t> idx(static_cast<size_t>(nrow + nmk));  // row indices, then the marker mask
   for (int b = 0; b < B; ++b) {
     for (int k = 0; k < K; ++k) {
       int64_t pp = marker_pos[static_cast<int64_t>(b) * K + k];
@@ -1037,15 +1039,17 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     idx[static_cast<size_t>(nmk + b)] =
         p.q_len[static_cast<size_t>(b)] > 0 ? p.seq_start[static_cast<size_t>(b)] : -1;
   }
-  tail_idx_.ensure(static_cast<size_t>(nrow) * 4);
+  for (int i = 0; i < nmk; ++i) idx[static_cast<size_t>(nrow + i)] = marker_mask[i] ? 1 : 0;
+  tail_idx_.ensure(idx.size() * 4);
   tail_rows_.ensure(static_cast<size_t>(nrow) * D * 4);
   tail_s0_.ensure(static_cast<size_t>(nmk) * D * 4);
   tail_s1_.ensure(static_cast<size_t>(nmk) * D * 4);
   tail_s2_.ensure(static_cast<size_t>(nmk) * 4);
-  tail_f4_.ensure(static_cast<size_t>(B) * 4 * 4);
+  tail_lg_.ensure(static_cast<size_t>(nmk) * 4);
   tail_ain_.ensure(static_cast<size_t>(B) * (D + 4) * 4);
   tail_ah_.ensure(static_cast<size_t>(B) * 256 * 4);
   tail_ao_.ensure(static_cast<size_t>(B) * n_act_ * 4);
+  tail_act_.ensure(static_cast<size_t>(B) * n_act_ * 4);
   hip_check(hipMemcpyAsync(tail_idx_.get(), idx.data(), idx.size() * 4, hipMemcpyHostToDevice, st),
             "upload marker rows");
   launch_gather_rows(X_.as<float>(), D, tail_idx_.as<int32_t>(), nrow, D, tail_rows_.as<float>(),
@@ -1089,49 +1093,9 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     g2.act = 0;
     gemm("scorer_linear2", g2, st);
   }
-  std::vector<float> s2(static_cast<size_t>(nmk));
-  hip_check(hipMemcpyAsync(s2.data(), tail_s2_.get(), s2.size() * 4, hipMemcpyDeviceToHost, st),
-            "download logits");
-  hip_check(hipStreamSynchronize(st), "forward: scorer");
-  for (int i = 0; i < nmk; ++i) logits[i] = marker_mask[i] ? s2[static_cast<size_t>(i)] : -1e4f;
-
-  // ---- act head (src/model.cpp:489-535): softmax statistics on host, MLP on device
-  std::vector<float> f4(static_cast<size_t>(B) * 4);
-  std::vector<double> pr(static_cast<size_t>(K));
-  for (int b = 0; b < B; ++b) {
-    const float* lg = logits + static_cast<int64_t>(b) * K;
-    float mx = lg[0];
-    for (int j = 1; j < K; ++j) mx = std::max(mx, lg[j]);
-    double s = 0;
-    for (int j = 0; j < K; ++j) {
-      pr[static_cast<size_t>(j)] = std::exp(lg[j] - mx);
-      s += pr[static_cast<size_t>(j)];
-    }
-    for (double& v : pr) v /= s;
-    double top1 = 0, top2 = 0;
-    for (double v : pr) {
-      if (v > top1) {
-        top2 = top1;
-        top1 = v;
-      } else if (v > top2) {
-        top2 = v;
-      }
-    }
-    double ksum = 0;
-    for (int k = 0; k < K; ++k) ksum += marker_mask[static_cast<int64_t>(b) * K + k];
-    const double kf = std::max(2.0, ksum);
-    double ent = 0;
-    for (double v : pr) ent -= v * std::log(std::max(v, 1e-9));
-    ent /= std::log(kf);
-    f4[static_cast<size_t>(b) * 4 + 0] = static_cast<float>(top1);
-    f4[static_cast<size_t>(b) * 4 + 1] = static_cast<float>(top1 - top2);
-    f4[static_cast<size_t>(b) * 4 + 2] = static_cast<float>(ent);
-    f4[static_cast<size_t>(b) * 4 + 3] = static_cast<float>(kf / 255.0);
-  }
-  hip_check(hipMemcpyAsync(tail_f4_.get(), f4.data(), f4.size() * 4, hipMemcpyHostToDevice, st),
-            "upload act features");
-  launch_concat_cols(tail_rows_.as<float>() + static_cast<size_t>(nmk) * D, D, tail_f4_.as<float>(),
-                     4, B, D, tail_ain_.as<float>(), D + 4, st);
+  launch_act_features(tail_s2_.as<float>(), tail_idx_.as<int32_t>() + nrow, B, K,
+                      tail_rows_.as<float>() + static_cast<size_t>(nmk) * D, D, D,
+                      tail_lg_.as<float>(), tail_ain_.as<float>(), D + 4, st);
   {
     GemmArgs g;
     g.A = tail_ain_.get();
@@ -1162,22 +1126,13 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     g2.act = 0;
     gemm("act_linear2", g2, st);
   }
-  std::vector<float> ao(static_cast<size_t>(B) * n_act_);
-  hip_check(hipMemcpyAsync(ao.data(), tail_ao_.get(), ao.size() * 4, hipMemcpyDeviceToHost, st),
+  launch_act_softmax(tail_ao_.as<float>(), B, n_act_, tail_act_.as<float>(), st);
+  hip_check(hipMemcpyAsync(logits, tail_lg_.get(), static_cast<size_t>(nmk) * 4, hipMemcpyDeviceToHost, st),
+            "download logits");
+  hip_check(hipMemcpyAsync(act, tail_act_.get(), static_cast<size_t>(B) * n_act_ * 4,
+                           hipMemcpyDeviceToHost, st),
             "download act");
-  hip_check(hipStreamSynchronize(st), "forward: act head");
-  for (int b = 0; b < B; ++b) {
-    float* a = ao.data() + static_cast<size_t>(b) * n_act_;
-    float amx = a[0];
-    for (int j = 1; j < n_act_; ++j) amx = std::max(amx, a[j]);
-    double as = 0;
-    for (int j = 0; j < n_act_; ++j) {
-      a[j] = std::exp(a[j] - amx);
-      as += a[j];
-    }
-    for (int j = 0; j < n_act_; ++j)
-      act[static_cast<size_t>(b) * n_act_ + j] = static_cast<float>(a[j] / as);
-  }
+  hip_check(hipStreamSynchronize(st), "forward: decision head");
   if (profile_) prof_collect();
 }
 

@@ -161,8 +161,8 @@ class Engine {
   DevBuf ids_, seqinfo_, tok_pos_, tok_seq_;
   DevBuf X_, Y_, QKV_, O_, G_, Z_;
   DevBuf splitk_;  // split-K partial sums for short batches (GemmArgs::partial)
-  DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_f4_, tail_ain_, tail_ah_,
-      tail_ao_;
+  DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_lg_, tail_ain_, tail_ah_,
+      tail_ao_, tail_act_;
   PinnedBuf h_stage_, h_out_;
   uint64_t ws_gen_ = 0;
 

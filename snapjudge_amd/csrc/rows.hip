@@ -403,16 +403,76 @@ __global__ void gather_rows_kernel(const float* src, int64_t ld_src, const int* 
     d[j] = s >= 0 ? src[static_cast<int64_t>(s) * ld_src + j] : 0.f;
 }
 
-__global__ void concat_cols_kernel(const float* src, int64_t ld_src, const float* extra, int E,
-                                   int n, int D, float* dst, int64_t ld_dst) {
-  const int i = blockIdx.x;
-  if (i >= n) return;
-  float* d = dst + static_cast<int64_t>(i) * ld_dst;
-  for (int j = threadIdx.x; j < D + E; j += blockDim.x)
-    d[j] = j < D ? src[static_cast<int64_t>(i) * ld_src + j] : extra[static_cast<int64_t>(i) * E + (j - D)];
+// Act-head inputs of row b (src/model.cpp:484, 489-517): the masked logits
+// (-1e4 where the marker is padding), their softmax (exp in float, sums in
+// double, as the reference), top1, top1 - top2, the entropy over log(max(2,
+// live markers)) and kf / 255, written after the row's [CLS] hidden state.
+// One workgroup per row; the short serial part runs on one lane.
+__global__ void act_features_kernel(const float* s2, const int* mmask, int K, const float* cls,
+                                    int64_t ld_cls, int D, float* logits, float* ain,
+                                    int64_t ld_ain) {
+  const int b = blockIdx.x;
+  const float* sb = s2 + static_cast<int64_t>(b) * K;
+  const int* mb = mmask + static_cast<int64_t>(b) * K;
+  float* lg = logits + static_cast<int64_t>(b) * K;
+  float* f = ain + static_cast<int64_t>(b) * ld_ain;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) lg[k] = mb[k] ? sb[k] : -1e4f;
+  for (int j = threadIdx.x; j < D; j += blockDim.x) f[j] = cls[static_cast<int64_t>(b) * ld_cls + j];
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  float mx = lg[0];
+  for (int j = 1; j < K; ++j) mx = fmaxf(mx, lg[j]);
+  double s = 0.0;
+  for (int j = 0; j < K; ++j) s += static_cast<double>(expf(lg[j] - mx));
+  double top1 = 0.0, top2 = 0.0, ent = 0.0, ksum = 0.0;
+  for (int j = 0; j < K; ++j) {
+    const double v = static_cast<double>(expf(lg[j] - mx)) / s;
+    if (v > top1) {
+      top2 = top1;
+      top1 = v;
+    } else if (v > top2) {
+      top2 = v;
+    }
+    ent -= v * log(fmax(v, 1e-9));
+    ksum += mb[j];
+  }
+  const double kf = fmax(2.0, ksum);
+  ent /= log(kf);
+  f[D + 0] = static_cast<float>(top1);
+  f[D + 1] = static_cast<float>(top1 - top2);
+  f[D + 2] = static_cast<float>(ent);
+  f[D + 3] = static_cast<float>(kf / 255.0);
+}
+
+// act = softmax(a) per row (src/model.cpp:523-534): exp in float, the sum in
+// double, each probability divided in double.  One thread per row.
+__global__ void act_softmax_kernel(const float* a, int B, int n, float* act) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const float* ab = a + static_cast<int64_t>(b) * n;
+  float amx = ab[0];
+  for (int j = 1; j < n; ++j) amx = fmaxf(amx, ab[j]);
+  double as = 0.0;
+  for (int j = 0; j < n; ++j) as += static_cast<double>(expf(ab[j] - amx));
+  for (int j = 0; j < n; ++j)
+    act[static_cast<int64_t>(b) * n + j] = static_cast<float>(static_cast<double>(expf(ab[j] - amx)) / as);
 }
 
 }  // namespace
+
+void launch_act_features(const float* s2, const int* mmask, int B, int K, const float* cls,
+                         int64_t ld_cls, int D, float* logits, float* ain, int64_t ld_ain,
+                         hipStream_t st) {
+  if (B <= 0 || K <= 0) return;
+  act_features_kernel<<<B, 256, 0, st>>>(s2, mmask, K, cls, ld_cls, D, logits, ain, ld_ain);
+  check_launch("act_features");
+}
+
+void launch_act_softmax(const float* a, int B, int n, float* act, hipStream_t st) {
+  if (B <= 0 || n <= 0) return;
+  act_softmax_kernel<<<(B + 63) / 64, 64, 0, st>>>(a, B, n, act);
+  check_launch("act_softmax");
+}
 
 void launch_ln(const LnArgs& a, hipStream_t st) {
   if (a.M <= 0) return;
@@ -487,13 +547,6 @@ void launch_gather_rows(const float* src, int64_t ld_src, const int* idx, int n,
   if (n <= 0) return;
   gather_rows_kernel<<<n, 256, 0, st>>>(src, ld_src, idx, n, D, dst, ld_dst);
   check_launch("gather_rows");
-}
-
-void launch_concat_cols(const float* src, int64_t ld_src, const float* extra, int E, int n, int D,
-                        float* dst, int64_t ld_dst, hipStream_t st) {
-  if (n <= 0) return;
-  concat_cols_kernel<<<n, 256, 0, st>>>(src, ld_src, extra, E, n, D, dst, ld_dst);
-  check_launch("concat_cols");
 }
 
 }  // namespace sjh

@@ -145,8 +145,13 @@ void launch_add_row_embedding(float* X, int64_t ldx, const float* table, const i
 void launch_gather_rows(const float* src, int64_t ld_src, const int* idx, int n, int D,
                         float* dst, int64_t ld_dst, hipStream_t st);
 
-// dst[i, :D] = src[i, :D]; dst[i, D:D+E] = extra[i, :E]   (fp32)
-void launch_concat_cols(const float* src, int64_t ld_src, const float* extra, int E, int n,
-                        int D, float* dst, int64_t ld_dst, hipStream_t st);
+// Decision-head tail on the device (src/model.cpp:484-534): per row b of B,
+// logits[b, k] = mmask[b, k] ? s2[b, k] : -1e4 and the act-head input
+// ain[b, :] = [cls[b, :D], top1, top1 - top2, entropy, kf / 255]
+void launch_act_features(const float* s2, const int* mmask, int B, int K, const float* cls,
+                         int64_t ld_cls, int D, float* logits, float* ain, int64_t ld_ain,
+                         hipStream_t st);
+// act[b, :] = softmax(a[b, :n]) with the reference's float exp / double sums
+void launch_act_softmax(const float* a, int B, int n, float* act, hipStream_t st);
 
 }  // namespace sjh
