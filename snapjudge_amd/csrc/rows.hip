@@ -210,7 +210,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
     // order: the split-K residual epilogue's arithmetic
     // (splits are loaded PG at a time, every load of a group issued before
     // the first add)
-    constexpr int PG = 4;
+    constexpr int PG = 8;
     const float* pr = a.parts + static_cast<int64_t>(r) * a.ld_part;
     float t[NV][4] = {};
     for (int s0 = 0; s0 < a.n_parts; s0 += PG) {
