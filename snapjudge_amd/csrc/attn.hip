@@ -150,14 +150,18 @@ __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
       for (int i = 0; i < 4; ++i)
         load_lds16((i < 2 ? kb : vb) + goff[i], base + (wave_s + 4 * i) * 1024);
     } else {
+      // rows clamped to the last key: the sequence's uniform base plus a
+      // 32-bit per-lane byte offset
+      const char* kq = reinterpret_cast<const char*>(K + row0 * a.ld_k);
+      const char* vq = reinterpret_cast<const char*>(V + row0 * a.ld_v);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int grp = wave_s + 4 * i;
         const int r = 8 * (grp & 7) + lrow;
-        const int key = min(k0 + r, klen - 1);
-        const bf16_t* src = (i < 2 ? K + (row0 + key) * a.ld_k : V + (row0 + key) * a.ld_v) +
-                            ((cslot ^ kv_swz(r)) << 3);
-        load_lds16(src, base + grp * 1024);
+        const uint32_t key = static_cast<uint32_t>(min(k0 + r, klen - 1));
+        const uint32_t off = key * static_cast<uint32_t>((i < 2 ? a.ld_k : a.ld_v) * 2) +
+                             ((cslot ^ kv_swz(r)) << 4);
+        load_lds16((i < 2 ? kq : vq) + off, base + grp * 1024);
       }
     }
   };
