@@ -94,6 +94,32 @@ def test_tiny_checkpoint_sliding_window(orc, golden_dir, prec):
 
 
 @pytest.mark.parametrize("prec", [FP32, BF16])
+def test_head_tail_masked_markers(orc, golden_dir, prec):
+    # decision-head tail on the device: a row with every marker masked (all
+    # logits -1e4, uniform softmax, kf = 2), a row with one live marker, and
+    # a marker position past L (clamped to L - 1) in a row without padding
+    rl, enc, w = synth.read_checkpoint(os.path.join(golden_dir, "tiny-ckpt"))
+    cfg = synth.flat_cfg(rl, enc)
+    ids, mask, lens = synth.make_batch(4, 32, 8, 32, cfg["vocab_size"], seed=9)
+    mask[3, :] = 1
+    lens[3] = 32
+    mp, mm, qt = synth.make_markers(lens, 4, [(0, 4), (1, 3), (2, 2), (0, 4)], seed=9)
+    mm[1, :] = 0
+    mm[2, :] = 0
+    mm[2, 0] = 1
+    mp[3, 2] = 1000
+    om = orc.model(w, cfg)
+    ref_lg, ref_act = om.forward(ids, mask, mp, mm, qt)
+    m = sj.Model(w, cfg, precision=prec)
+    lg, act = m.forward(ids, mask, mp, mm, qt)
+    assert np.all(lg[mm == 0] == np.float32(-1e4))
+    live = [b for b in range(len(mm)) if mm[b].sum() > 0]
+    assert probs_err(orc, lg[live], ref_lg[live], mm[live]) <= 5e-3
+    assert float(np.abs(act - ref_act).max()) <= 5e-3
+    m.close()
+
+
+@pytest.mark.parametrize("prec", [FP32, BF16])
 def test_sliding_lora_model(orc, prec):
     rl, enc, w = synth.make_model(hidden_size=128, num_hidden_layers=3, num_attention_heads=2,
                                   intermediate_size=192, vocab_size=1000, store="BF16",
