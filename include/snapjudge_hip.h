@@ -143,6 +143,14 @@ int sjh_model_encode_device(sjh_model* m, const int32_t* d_ids, const int32_t* h
 int sjh_model_info(const sjh_model* m, int32_t* D, int32_t* H, int32_t* n_act,
                    int32_t* precision);
 
+/* Graph cache of a model (use_graphs): graphs held now, captures and replays
+ * so far.  A batch is replayed from the graph of its shape bucket (batch size
+ * rounded up to a power of two, token count and longest row rounded up), so a
+ * serving loop captures once per bucket.  No counterpart in the reference,
+ * whose graph map is private (cuda/fast.cpp:376-393). */
+int sjh_model_graph_stats(const sjh_model* m, int32_t* cached, int64_t* captures,
+                          int64_t* replays);
+
 /* Enable/disable per-kernel timing with hipEvents on the model's launches and
  * read the totals: names[i] (static strings), total_ms[i], launches[i]. */
 int sjh_model_profile(sjh_model* m, int32_t enable);

@@ -72,6 +72,7 @@ _SIGS = {
     "sjh_model_encode_device": (C.c_int, [C.c_void_p, C.c_void_p, _i32p, C.c_int32, C.c_void_p,
                                           C.c_void_p]),
     "sjh_model_info": (C.c_int, [C.c_void_p, _i32p, _i32p, _i32p, _i32p]),
+    "sjh_model_graph_stats": (C.c_int, [C.c_void_p, _i32p, _i64p, _i64p]),
     "sjh_model_profile": (C.c_int, [C.c_void_p, C.c_int32]),
     "sjh_model_profile_read": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_char_p),
                                          C.POINTER(C.c_double), _i64p, _i32p]),
@@ -274,6 +275,11 @@ class Model:
         lens = np.ascontiguousarray(lens, dtype=np.int32)
         check(lib().sjh_model_encode_device(self._h, C.c_void_p(d_ids), lens.ctypes.data_as(_i32p),
                                             len(lens), C.c_void_p(d_hidden), C.c_void_p(stream)))
+
+    def graph_stats(self) -> dict:
+        n, cap, rep = C.c_int32(), C.c_int64(), C.c_int64()
+        check(lib().sjh_model_graph_stats(self._h, C.byref(n), C.byref(cap), C.byref(rep)))
+        return {"cached": n.value, "captures": cap.value, "replays": rep.value}
 
     def profile(self, on: bool):
         check(lib().sjh_model_profile(self._h, 1 if on else 0))

@@ -135,6 +135,14 @@ int sjh_model_info(const sjh_model* m, int32_t* D, int32_t* H, int32_t* n_act,
   });
 }
 
+int sjh_model_graph_stats(const sjh_model* m, int32_t* cached, int64_t* captures,
+                          int64_t* replays) {
+  return guarded([&] {
+    if (!m) sjh::fail("null model");
+    m->eng->graph_stats(cached, captures, replays);
+  });
+}
+
 int sjh_model_profile(sjh_model* m, int32_t enable) {
   return guarded([&] {
     if (!m) sjh::fail("null model");

@@ -98,13 +98,6 @@ void quantize_fp8_rows(const float* w, size_t rows, size_t cols, uint8_t* q, flo
 }
 
 namespace {
-// Per-batch sequence table on the device: five arrays of B ints (seq_start,
-// q_len, k_len, qtype, order), padded to a 16-byte boundary, then B
-// {seq_start, q_len, k_len, 0} quadruples in attention order.
-size_t seqinfo_meta_off(int B) { return (static_cast<size_t>(5) * B + 3) / 4 * 4; }
-size_t seqinfo_ints(int B) { return seqinfo_meta_off(B) + static_cast<size_t>(4) * B; }
-
-
 uint16_t bf16_rne(float f) {
   uint32_t u;
   std::memcpy(&u, &f, 4);
@@ -220,6 +213,8 @@ Engine::Engine(const sjh_model_desc& d, const sjh_options& o) {
   max_len_ = o.max_len > 0 ? std::min(o.max_len, max_pos_) : max_pos_;
 
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  hip_check(hipEventCreateWithFlags(&ev_done_, hipEventDisableTiming), "hipEventCreate");
+  hip_check(hipEventCreateWithFlags(&ev_upload_, hipEventDisableTiming), "hipEventCreate");
   stage_weights(d);
 }
 
@@ -233,7 +228,10 @@ Engine::~Engine() {
     (void)hipEventDestroy(p.b);
   }
   for (hipEvent_t e : ev_pool_) (void)hipEventDestroy(e);
+  if (done_recorded_) (void)hipEventSynchronize(ev_done_);
   if (ev_null_) (void)hipEventDestroy(ev_null_);
+  if (ev_done_) (void)hipEventDestroy(ev_done_);
+  if (ev_upload_) (void)hipEventDestroy(ev_upload_);
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -324,6 +322,7 @@ void Engine::stage_weights(const sjh_model_desc& d) {
   act_b2_ = upload_f32(d.act_b2, static_cast<size_t>(n_act_), "act b2");
 }
 
+
 // ------------------------------------------------------------------ batches --
 namespace {
 // Longest sequences first: attention workgroups of a long sequence run
@@ -334,6 +333,52 @@ void set_order(BatchPlan& p) {
   std::stable_sort(p.order.begin(), p.order.end(), [&](int32_t x, int32_t y) {
     return p.q_len[static_cast<size_t>(x)] > p.q_len[static_cast<size_t>(y)];
   });
+}
+
+int round_up(int x, int g) { return (x + g - 1) / g * g; }
+
+// The launch bucket of a batch (see BatchPlan).  Launches are sized for the
+// bucket and every kernel stops at the batch's own token count, read from the
+// device table, so the results depend on the bucket only through the choice
+// of GEMM tiling; graph replay and direct launches share the same plan.
+void set_bucket(BatchPlan& p) {
+  int bb = 1;
+  while (bb < p.B) bb <<= 1;
+  p.Bb = bb;
+  if (p.T <= 1024) {
+    p.Tb = round_up(std::max(p.T, 1), 64);
+  } else {
+    int lg = 0;
+    while ((2 << lg) <= p.T) ++lg;  // 2^lg <= T < 2^(lg+1)
+    p.Tb = round_up(p.T, 1 << (lg - 3));
+  }
+  p.max_qb = p.max_q <= 1024 ? round_up(std::max(p.max_q, 1), 128) : round_up(p.max_q, 1024);
+}
+
+// The sequence table (layout in sjh_kernels.hpp) of a plan, on the host.
+void fill_seq_table(const BatchPlan& p, const int32_t* qtype, int32_t* t) {
+  const int Bb = p.Bb;
+  t[0] = p.T;
+  t[1] = p.B;
+  t[2] = t[3] = 0;
+  int32_t* seq_start = t + kSeqHdr;
+  for (int b = 0; b < Bb; ++b) {
+    const bool real = b < p.B;
+    const size_t u = static_cast<size_t>(b);
+    seq_start[b] = real ? p.seq_start[u] : p.T;
+    seq_start[Bb + b] = real ? p.q_len[u] : 0;
+    seq_start[2 * Bb + b] = real ? p.k_len[u] : 0;
+    seq_start[3 * Bb + b] = real && qtype ? qtype[b] : 0;
+    seq_start[4 * Bb + b] = real ? p.order[u] : b;
+  }
+  int32_t* meta = t + seq_table_meta(Bb);
+  for (int z = 0; z < Bb; ++z) {
+    const int b = seq_start[4 * Bb + z];
+    meta[4 * z + 0] = seq_start[b];
+    meta[4 * z + 1] = seq_start[Bb + b];
+    meta[4 * z + 2] = seq_start[2 * Bb + b];
+    meta[4 * z + 3] = 0;
+  }
 }
 }  // namespace
 
@@ -364,6 +409,7 @@ BatchPlan Engine::plan(const int64_t* ids, const int64_t* mask, int B, int L,
   p.max_q = 0;
   for (int b = 0; b < B; ++b) p.max_q = std::max(p.max_q, p.q_len[static_cast<size_t>(b)]);
   set_order(p);
+  set_bucket(p);
   if (ids_out) {
     for (int b = 0; b < B; ++b) {
       const int rows = p.q_len[static_cast<size_t>(b)];
@@ -377,17 +423,42 @@ BatchPlan Engine::plan(const int64_t* ids, const int64_t* mask, int B, int L,
   return p;
 }
 
-void Engine::ensure_workspace(int T, int B) {
-  if (T <= cap_T_ && B <= cap_B_) return;
-  hip_check(hipStreamSynchronize(stream_), "sync before workspace growth");
-  const int nT = std::max(T, cap_T_ + cap_T_ / 4);
-  const int nB = std::max(B, cap_B_);
+BatchPlan Engine::plan_lens(const int32_t* h_lens, int B) const {
+  BatchPlan p;
+  p.B = B;
+  p.seq_start.resize(static_cast<size_t>(B));
+  p.q_len.resize(static_cast<size_t>(B));
+  p.k_len.resize(static_cast<size_t>(B));
+  int64_t T = 0;
+  for (int b = 0; b < B; ++b) {
+    const int n = h_lens[b];
+    if (n < 0 || n > max_len_) fail("sequence length outside [0, max_len]");
+    p.seq_start[static_cast<size_t>(b)] = static_cast<int32_t>(T);
+    p.q_len[static_cast<size_t>(b)] = n;
+    p.k_len[static_cast<size_t>(b)] = n;
+    p.max_q = std::max(p.max_q, n);
+    T += n;
+  }
+  if (T > (int64_t{1} << 30)) fail("batch too large");
+  p.T = static_cast<int>(T);
+  p.L = p.max_q;
+  set_order(p);
+  set_bucket(p);
+  return p;
+}
+
+void Engine::ensure_workspace(int Tb, int Bb) {
+  if (Tb <= cap_T_ && Bb <= cap_B_) return;
+  // every earlier call's work (on any stream) has finished with the old buffers
+  if (done_recorded_) hip_check(hipEventSynchronize(ev_done_), "sync before workspace growth");
+  const int nT = std::max(Tb, cap_T_ + cap_T_ / 4);
+  const int nB = std::max(Bb, cap_B_);
   const size_t t = static_cast<size_t>(std::max(nT, 1));
   const size_t D = D_, as = dt_size(act_dt_);
   ids_.ensure(t * 4);
   tok_pos_.ensure(t * 4);
   tok_seq_.ensure(t * 4);
-  seqinfo_.ensure(seqinfo_ints(std::max(nB, 1)) * 4);
+  seqinfo_.ensure(seq_table_ints(std::max(nB, 1)) * 4);
   X_.ensure(t * D * 4);
   Y_.ensure(t * D * as);
   QKV_.ensure(t * 3 * D * as);
@@ -401,6 +472,16 @@ void Engine::ensure_workspace(int T, int B) {
   }
   cap_T_ = nT;
   cap_B_ = nB;
+  ws_.seq = seqinfo_.as<int32_t>();
+  ws_.tok_pos = tok_pos_.as<int>();
+  ws_.tok_seq = tok_seq_.as<int>();
+  ws_.Y = Y_.get();
+  ws_.QKV = QKV_.get();
+  ws_.O = O_.get();
+  ws_.G = G_.get();
+  ws_.Z = Z_.as<float>();
+  ws_.partial = splitk_.as<float>();
+  ws_.partial_cap = static_cast<int64_t>(splitk_.bytes() / 4);
   ++ws_gen_;
   for (auto& kv : graphs_)
     if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
@@ -409,25 +490,13 @@ void Engine::ensure_workspace(int T, int B) {
 
 void Engine::upload_batch(const BatchPlan& p, const int32_t* h_ids, const int32_t* h_qtype,
                           hipStream_t st) {
-  // pinned staging: [seq_start | q_len | k_len | qtype | order | pad to 16 B |
-  // meta] then the token ids; meta[z] = {seq_start, q_len, k_len, 0} of the
-  // z-th sequence in attention order, one 16-byte load for a workgroup
-  const size_t nsi = seqinfo_ints(p.B);
+  // pinned staging: the sequence table, then the token ids.  The previous
+  // copy out of the buffer (possibly on another stream) must be done first.
+  const size_t nsi = seq_table_ints(p.Bb);
+  if (upload_recorded_) hip_check(hipEventSynchronize(ev_upload_), "staging buffer reuse");
   h_stage_.ensure((nsi + (h_ids ? p.T : 0)) * 4);
   int32_t* s = h_stage_.as<int32_t>();
-  std::memcpy(s, p.seq_start.data(), p.B * 4);
-  std::memcpy(s + p.B, p.q_len.data(), p.B * 4);
-  std::memcpy(s + 2 * p.B, p.k_len.data(), p.B * 4);
-  for (int b = 0; b < p.B; ++b) s[3 * p.B + b] = h_qtype ? h_qtype[b] : 0;
-  std::memcpy(s + 4 * p.B, p.order.data(), p.B * 4);
-  int32_t* meta = s + seqinfo_meta_off(p.B);
-  for (int z = 0; z < p.B; ++z) {
-    const size_t b = static_cast<size_t>(p.order[static_cast<size_t>(z)]);
-    meta[4 * z + 0] = p.seq_start[b];
-    meta[4 * z + 1] = p.q_len[b];
-    meta[4 * z + 2] = p.k_len[b];
-    meta[4 * z + 3] = 0;
-  }
+  fill_seq_table(p, h_qtype, s);
   hip_check(hipMemcpyAsync(seqinfo_.get(), s, nsi * 4, hipMemcpyHostToDevice, st), "upload seqinfo");
   if (h_ids) {
     std::memcpy(s + nsi, h_ids, static_cast<size_t>(p.T) * 4);
@@ -435,6 +504,27 @@ void Engine::upload_batch(const BatchPlan& p, const int32_t* h_ids, const int32_
                              hipMemcpyHostToDevice, st),
               "upload ids");
   }
+  hip_check(hipEventRecord(ev_upload_, st), "record upload");
+  upload_recorded_ = true;
+}
+
+void Engine::set_seq_table(const BatchPlan& p, const int32_t* h_lens, int32_t* table,
+                           hipStream_t st) {
+  if (p.Bb <= kSeqTableMaxB) {
+    launch_seq_table(h_lens, p.B, p.Bb, table, st);
+  } else {
+    require(table == seqinfo_.as<int32_t>(), "sequence table: more than 256 sequences need the workspace");
+    upload_batch(p, nullptr, nullptr, st);
+  }
+}
+
+void Engine::begin_call(hipStream_t st) {
+  if (done_recorded_) hip_check(hipStreamWaitEvent(st, ev_done_, 0), "order after the previous call");
+}
+
+void Engine::end_call(hipStream_t st) {
+  hip_check(hipEventRecord(ev_done_, st), "record call end");
+  done_recorded_ = true;
 }
 
 // ------------------------------------------------------------------ launches --
@@ -488,6 +578,13 @@ void Engine::set_profile(bool on) {
   if (on) prof_tot_.clear();
 }
 
+void Engine::graph_stats(int32_t* cached, int64_t* captures, int64_t* replays) {
+  std::lock_guard<std::mutex> lk(mu_);
+  if (cached) *cached = static_cast<int32_t>(graphs_.size());
+  if (captures) *captures = n_captures_;
+  if (replays) *replays = n_replays_;
+}
+
 std::vector<std::tuple<const char*, double, int64_t>> Engine::profile_totals() {
   std::lock_guard<std::mutex> lk(mu_);
   hip_check(hipSetDevice(dev_), "hipSetDevice");
@@ -497,31 +594,35 @@ std::vector<std::tuple<const char*, double, int64_t>> Engine::profile_totals() {
   return v;
 }
 
-void Engine::gemm(const char* name, const GemmArgs& g0, hipStream_t st) {
+void Engine::gemm(const char* name, const GemmArgs& g0, const Ws& w, hipStream_t st) {
   GemmArgs g = g0;
-  g.partial = splitk_.as<float>();
-  g.partial_cap = static_cast<int64_t>(splitk_.bytes() / 4);
+  g.partial = w.partial;
+  g.partial_cap = w.partial_cap;
   prof_begin(st);
   launch_gemm(g, st);
   prof_end(name, st);
 }
 
 void Engine::resid_gemm_ln(const char* gname, const GemmArgs& g0, const char* lname, LnArgs a,
-                           hipStream_t st) {
+                           const Ws& w, hipStream_t st) {
   GemmArgs g = g0;
-  g.partial = splitk_.as<float>();
-  g.partial_cap = static_cast<int64_t>(splitk_.bytes() / 4);
+  g.partial = w.partial;
+  g.partial_cap = w.partial_cap;
+  // the layer norm that would add the splits: X rows written back in place
+  LnArgs folded = a;
+  folded.parts = g.partial;
+  folded.part_stride = static_cast<int64_t>(g.M) * g.N;
+  folded.ld_part = g.N;
+  folded.part_bias = g.bias;
+  folded.xio = g.X;
+  folded.n_parts = 1;
   prof_begin(st);
-  const int S = g.M <= 256 ? launch_gemm_resid_partials(g, st) : 0;
+  const int S = g.M <= 256 && ln_takes_parts(folded) ? launch_gemm_resid_partials(g, st) : 0;
   if (S == 0) launch_gemm(g, st);
   prof_end(gname, st);
   if (S > 0) {  // X is updated by the layer norm: X += sum of the splits (+ bias)
-    a.parts = g.partial;
-    a.n_parts = S;
-    a.part_stride = static_cast<int64_t>(g.M) * g.N;
-    a.ld_part = g.N;
-    a.part_bias = g.bias;
-    a.xio = g.X;
+    folded.n_parts = S;
+    a = folded;
   }
   ln(lname, a, st);
 }
@@ -539,19 +640,23 @@ void Engine::attn(const char* name, const AttnArgs& a, hipStream_t st) {
 }
 
 // ------------------------------------------------------------------ encoder --
-void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X, hipStream_t st) {
-  const int T = p.T, D = D_, F = F_;
-  const int32_t* si = seqinfo_.as<int32_t>();
-  const int32_t* seq_start = si;
-  const int32_t* q_len = si + p.B;
-  const int32_t* k_len = si + 2 * p.B;
+// Launch sizes come from the plan's bucket (Tb rows, Bb table entries, max_qb
+// queries); every kernel reads the real token count from the table's header.
+void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_ids, float* X,
+                             hipStream_t st) {
+  const int T = p.Tb, D = D_, F = F_, Bb = p.Bb;
+  const int32_t* si = w.seq;
+  const int* T_dev = si;  // header[0]
+  const int32_t* seq_start = si + kSeqHdr;
+  const int32_t* q_len = seq_start + Bb;
+  const int32_t* k_len = seq_start + 2 * Bb;
   const int adt = act_dt_;
-  void* Y = Y_.get();
-  void* QKV = QKV_.get();
-  void* O = O_.get();
-  void* G = G_.get();
+  void* Y = w.Y;
+  void* QKV = w.QKV;
+  void* O = w.O;
+  void* G = w.G;
 
-  launch_token_index(seq_start, q_len, p.B, tok_pos_.as<int>(), tok_seq_.as<int>(), st);
+  launch_token_index(seq_start, q_len, Bb, w.tok_pos, w.tok_seq, st);
 
   // src/model.cpp:332-340: X = LN(emb[ids]); layer 0 reads X itself
   {
@@ -570,6 +675,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       e.ld_y = D;
     }
     e.M = T;
+    e.M_dev = T_dev;
     e.D = D;
     ln("emb_ln", e, st);
   }
@@ -590,6 +696,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
     a.y_dtype = adt;
     a.ld_y = D;
     a.M = T;
+    a.M_dev = T_dev;
     a.D = D;
     return a;
   };
@@ -603,6 +710,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
   final_args.x_out = X;
   final_args.ld_x = D;
   final_args.M = T;
+  final_args.M_dev = T_dev;
   final_args.D = D;
   for (int li = 0; li < nlayers_; ++li) {
     const LayerDev& ly = layers_[static_cast<size_t>(li)];
@@ -617,6 +725,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       if (w8_) g.w_dtype = DT_FP8, g.w_scale = ly.wqkv_s.as<float>();
       g.ldw = D;
       g.M = T;
+      g.M_dev = T_dev;
       g.N = 3 * D;
       g.K = D;
       g.in_dtype = adt;
@@ -624,13 +733,13 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.out = QKV;
       g.ldo = 3 * D;
       g.out_dtype = adt;
-      g.pos = tok_pos_.as<int>();
+      g.pos = w.tok_pos;
       g.rope_cos = (ly.sliding ? rope_cos_slide_ : rope_cos_full_).as<float>();
       g.rope_sin = (ly.sliding ? rope_sin_slide_ : rope_sin_full_).as<float>();
       g.rope_rows = max_pos_;
       g.rope_dim = D;
       g.head_dim = Dh_;
-      gemm("gemm_qkv_rope", g, st);
+      gemm("gemm_qkv_rope", g, w, st);
     }
     {  // attention (src/model.cpp:381)
       AttnArgs a;
@@ -644,12 +753,12 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       a.seq_start = seq_start;
       a.q_len = q_len;
       a.k_len = k_len;
-      a.seq_order = si + 4 * p.B;
-      a.seq_meta = si + seqinfo_meta_off(p.B);
-      a.B = p.B;
+      a.seq_order = seq_start + 4 * Bb;
+      a.seq_meta = si + seq_table_meta(Bb);
+      a.B = Bb;
       a.H = H_;
       a.Dh = Dh_;
-      a.max_q = p.max_q;
+      a.max_q = p.max_qb;
       a.window = ly.window;
       a.scale = scale;
       attn("attention", a, st);
@@ -662,6 +771,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       if (w8_) g.w_dtype = DT_FP8, g.w_scale = ly.wo_s.as<float>();
       g.ldw = D;
       g.M = T;
+      g.M_dev = T_dev;
       g.N = D;
       g.K = D;
       g.in_dtype = adt;
@@ -679,8 +789,9 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       a.y_dtype = adt;
       a.ld_y = D;
       a.M = T;
+      a.M_dev = T_dev;
       a.D = D;
-      resid_gemm_ln("gemm_wo_resid", g, "mlp_norm", a, st);
+      resid_gemm_ln("gemm_wo_resid", g, "mlp_norm", a, w, st);
     }
     {  // G = geglu(Y . Wi^T) (src/model.cpp:394)
       GemmArgs g;
@@ -690,6 +801,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       if (w8_) g.w_dtype = DT_FP8, g.w_scale = ly.wi_s.as<float>();
       g.ldw = D;
       g.M = T;
+      g.M_dev = T_dev;
       g.N = F;
       g.K = D;
       g.in_dtype = adt;
@@ -697,7 +809,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.out = G;
       g.ldo = F;
       g.out_dtype = adt;
-      gemm("gemm_wi_geglu", g, st);
+      gemm("gemm_wi_geglu", g, w, st);
     }
     {  // X += G . Wo2^T (src/model.cpp:395-397)
       GemmArgs g;
@@ -707,6 +819,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       if (w8_) g.w_dtype = DT_FP8, g.w_scale = ly.wo2_s.as<float>();
       g.ldw = F;
       g.M = T;
+      g.M_dev = T_dev;
       g.N = D;
       g.K = F;
       g.in_dtype = adt;
@@ -715,9 +828,9 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
       g.ldx = D;
       // then the next layer's attn_norm, or the final norm
       if (li + 1 < nlayers_)
-        resid_gemm_ln("gemm_wo2_resid", g, "attn_norm", attn_norm_args(li + 1), st);
+        resid_gemm_ln("gemm_wo2_resid", g, "attn_norm", attn_norm_args(li + 1), w, st);
       else
-        resid_gemm_ln("gemm_wo2_resid", g, "final_norm", final_args, st);
+        resid_gemm_ln("gemm_wo2_resid", g, "final_norm", final_args, w, st);
     }
   }
   if (lora_r_ > 0) {  // h += (h . A^T) . B^T (src/model.cpp:402-407)
@@ -727,37 +840,41 @@ void Engine::enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X,
     g.W = lora_a_.get();
     g.ldw = D;
     g.M = T;
+    g.M_dev = T_dev;
     g.N = lora_r_;
     g.K = D;
     g.in_dtype = DT_F32;
     g.epi = EPI_STORE;
-    g.out = Z_.get();
+    g.out = w.Z;
     g.ldo = lora_r_;
     g.out_dtype = DT_F32;
-    gemm("gemm_lora_a", g, st);
+    gemm("gemm_lora_a", g, w, st);
     GemmArgs g2;
-    g2.A = Z_.get();
+    g2.A = w.Z;
     g2.lda = lora_r_;
     g2.W = lora_b_.get();
     g2.ldw = lora_r_;
     g2.M = T;
+    g2.M_dev = T_dev;
     g2.N = D;
     g2.K = lora_r_;
     g2.in_dtype = DT_F32;
     g2.epi = EPI_RESID;
     g2.X = X;
     g2.ldx = D;
-    gemm("gemm_lora_b", g2, st);
+    gemm("gemm_lora_b", g2, w, st);
   }
 }
 
 // src/model.cpp:409-459: type embedding, then N pre-norm TransformerEncoderLayers.
-void Engine::enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st) {
-  const int T = p.T, D = D_;
-  const int32_t* si = seqinfo_.as<int32_t>();
+void Engine::enqueue_head_layers(const BatchPlan& p, const Ws& w, float* X, hipStream_t st) {
+  const int T = p.Tb, D = D_, Bb = p.Bb;
+  const int32_t* si = w.seq;
+  const int* T_dev = si;
+  const int32_t* seq_start = si + kSeqHdr;
   const int adt = act_dt_;
-  launch_add_row_embedding(X, D, type_emb_.as<float>(), si + 3 * p.B, tok_seq_.as<int>(), T, D,
-                           st);
+  launch_add_row_embedding(X, D, type_emb_.as<float>(), seq_start + 3 * Bb, w.tok_seq, T, T_dev,
+                           D, st);
   const float scale = 1.0f / std::sqrt(static_cast<float>(Dh_));
   for (const HeadDev& hd : head_) {
     LnArgs a;
@@ -767,56 +884,59 @@ void Engine::enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st) {
     a.w = hd.n1w.as<float>();
     a.b = hd.n1b.as<float>();
     a.eps = 1e-5f;
-    a.y_out = Y_.get();
+    a.y_out = w.Y;
     a.y_dtype = adt;
     a.ld_y = D;
     a.M = T;
+    a.M_dev = T_dev;
     a.D = D;
     ln("head_norm1", a, st);
 
     GemmArgs g;
-    g.A = Y_.get();
+    g.A = w.Y;
     g.lda = D;
     g.W = hd.in_w.get();
     g.ldw = D;
     g.M = T;
+    g.M_dev = T_dev;
     g.N = 3 * D;
     g.K = D;
     g.in_dtype = adt;
     g.epi = EPI_STORE;
-    g.out = QKV_.get();
+    g.out = w.QKV;
     g.ldo = 3 * D;
     g.out_dtype = adt;
     g.bias = hd.in_b.as<float>();
-    gemm("head_in_proj", g, st);
+    gemm("head_in_proj", g, w, st);
 
     AttnArgs at;
-    at.q = QKV_.get();
-    at.k = off<char>(QKV_.get(), D, adt);
-    at.v = off<char>(QKV_.get(), 2 * D, adt);
+    at.q = w.QKV;
+    at.k = off<char>(w.QKV, D, adt);
+    at.v = off<char>(w.QKV, 2 * D, adt);
     at.ld_q = at.ld_k = at.ld_v = 3 * D;
-    at.o = O_.get();
+    at.o = w.O;
     at.ld_o = D;
     at.dtype = adt;
-    at.seq_start = si;
-    at.q_len = si + p.B;
-    at.k_len = si + 2 * p.B;
-    at.seq_order = si + 4 * p.B;
-    at.seq_meta = si + seqinfo_meta_off(p.B);
-    at.B = p.B;
+    at.seq_start = seq_start;
+    at.q_len = seq_start + Bb;
+    at.k_len = seq_start + 2 * Bb;
+    at.seq_order = seq_start + 4 * Bb;
+    at.seq_meta = si + seq_table_meta(Bb);
+    at.B = Bb;
     at.H = H_;
     at.Dh = Dh_;
-    at.max_q = p.max_q;
+    at.max_q = p.max_qb;
     at.window = 0;
     at.scale = scale;
     attn("head_attention", at, st);
 
     GemmArgs go;
-    go.A = O_.get();
+    go.A = w.O;
     go.lda = D;
     go.W = hd.out_w.get();
     go.ldw = D;
     go.M = T;
+    go.M_dev = T_dev;
     go.N = D;
     go.K = D;
     go.in_dtype = adt;
@@ -824,7 +944,7 @@ void Engine::enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st) {
     go.X = X;
     go.ldx = D;
     go.bias = hd.out_b.as<float>();
-    gemm("head_out_proj", go, st);
+    gemm("head_out_proj", go, w, st);
 
     LnArgs a2 = a;
     a2.w = hd.n2w.as<float>();
@@ -832,28 +952,30 @@ void Engine::enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st) {
     ln("head_norm2", a2, st);
 
     GemmArgs g1;
-    g1.A = Y_.get();
+    g1.A = w.Y;
     g1.lda = D;
     g1.W = hd.l1w.get();
     g1.ldw = D;
     g1.M = T;
+    g1.M_dev = T_dev;
     g1.N = 4 * D;
     g1.K = D;
     g1.in_dtype = adt;
     g1.epi = EPI_STORE;
-    g1.out = G_.get();
+    g1.out = w.G;
     g1.ldo = 4 * D;
     g1.out_dtype = adt;
     g1.bias = hd.l1b.as<float>();
     g1.act = 2;
-    gemm("head_linear1", g1, st);
+    gemm("head_linear1", g1, w, st);
 
     GemmArgs g2;
-    g2.A = G_.get();
+    g2.A = w.G;
     g2.lda = 4 * D;
     g2.W = hd.l2w.get();
     g2.ldw = 4 * D;
     g2.M = T;
+    g2.M_dev = T_dev;
     g2.N = D;
     g2.K = 4 * D;
     g2.in_dtype = adt;
@@ -861,25 +983,27 @@ void Engine::enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st) {
     g2.X = X;
     g2.ldx = D;
     g2.bias = hd.l2b.as<float>();
-    gemm("head_linear2", g2, st);
+    gemm("head_linear2", g2, w, st);
   }
 }
 
-void Engine::run_device(const BatchPlan& p, const int32_t* d_ids, float* X, bool head,
-                        hipStream_t st) {
-  enqueue_encoder(p, d_ids, X, st);
-  if (head) enqueue_head_layers(p, X, st);
+void Engine::run_device(const BatchPlan& p, const Ws& w, const int32_t* d_ids, float* X,
+                        bool head, hipStream_t st) {
+  enqueue_encoder(p, w, d_ids, X, st);
+  if (head) enqueue_head_layers(p, w, X, st);
 }
 
 void Engine::run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, float* X,
                                     bool head, hipStream_t st) {
   if (!use_graphs_ || profile_) {
-    run_device(p, d_ids, X, head, st);
+    run_device(p, ws_, d_ids, X, head, st);
     return;
   }
-  const std::vector<int64_t> key = {p.B,
-                                    p.T,
-                                    p.max_q,
+  // one graph per bucket and buffer set: the batch's own sizes and lengths
+  // reach the kernels through the sequence table, written before the launch
+  const std::vector<int64_t> key = {p.Bb,
+                                    p.Tb,
+                                    p.max_qb,
                                     head ? 1 : 0,
                                     static_cast<int64_t>(ws_gen_),
                                     reinterpret_cast<int64_t>(d_ids),
@@ -887,15 +1011,17 @@ void Engine::run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, fl
                                     reinterpret_cast<int64_t>(st)};
   auto it = graphs_.find(key);
   if (it == graphs_.end()) {
-    if (graphs_.size() >= 32) {
-      for (auto& kv : graphs_)
-        if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
-      graphs_.clear();
+    if (graphs_.size() >= kMaxGraphs) {  // evict the least recently used graph
+      auto lru = graphs_.begin();
+      for (auto jt = graphs_.begin(); jt != graphs_.end(); ++jt)
+        if (jt->second.last_use < lru->second.last_use) lru = jt;
+      if (lru->second.exec) (void)hipGraphExecDestroy(lru->second.exec);
+      graphs_.erase(lru);
     }
     hipGraph_t graph = nullptr;
     hip_check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
     try {
-      run_device(p, d_ids, X, head, st);
+      run_device(p, ws_, d_ids, X, head, st);
     } catch (...) {
       (void)hipStreamEndCapture(st, &graph);
       if (graph) (void)hipGraphDestroy(graph);
@@ -907,7 +1033,11 @@ void Engine::run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, fl
     (void)hipGraphDestroy(graph);
     hip_check(e, "graph instantiate");
     it = graphs_.emplace(key, g).first;
+    ++n_captures_;
+  } else {
+    ++n_replays_;
   }
+  it->second.last_use = ++graph_clock_;
   hip_check(hipGraphLaunch(it->second.exec, st), "graph launch");
 }
 
@@ -921,25 +1051,29 @@ void Engine::encode(const int64_t* ids, const int64_t* mask, int B, int L, float
   BatchPlan p0 = plan(ids, mask, B, L, nullptr);
   packed.resize(static_cast<size_t>(p0.T));
   BatchPlan p = plan(ids, mask, B, L, packed.data());
-  ensure_workspace(std::max(p.T, 1), B);
+  ensure_workspace(p.Tb, p.Bb);
   const size_t D = D_;
+  hipStream_t st = stream_;
+  begin_call(st);
   if (p.T > 0) {
-    upload_batch(p, packed.data(), nullptr, stream_);
-    run_device_maybe_graph(p, ids_.as<int32_t>(), X_.as<float>(), false, stream_);
+    upload_batch(p, packed.data(), nullptr, st);
+    run_device_maybe_graph(p, ids_.as<int32_t>(), X_.as<float>(), false, st);
   }
   if (pad_rows_) {
     if (p.T > 0)
       hip_check(hipMemcpyAsync(hidden, X_.get(), static_cast<size_t>(p.T) * D * 4,
-                               hipMemcpyDeviceToHost, stream_),
+                               hipMemcpyDeviceToHost, st),
                 "download hidden");
-    hip_check(hipStreamSynchronize(stream_), "encode");
+    end_call(st);
+    hip_check(hipStreamSynchronize(st), "encode");
   } else {
     h_out_.ensure(std::max<size_t>(static_cast<size_t>(p.T) * D * 4, 4));
     if (p.T > 0)
       hip_check(hipMemcpyAsync(h_out_.as<float>(), X_.get(), static_cast<size_t>(p.T) * D * 4,
-                               hipMemcpyDeviceToHost, stream_),
+                               hipMemcpyDeviceToHost, st),
                 "download hidden");
-    hip_check(hipStreamSynchronize(stream_), "encode");
+    end_call(st);
+    hip_check(hipStreamSynchronize(st), "encode");
     std::memset(hidden, 0, static_cast<size_t>(B) * L * D * 4);
     const float* src = h_out_.as<float>();
     for (int b = 0; b < B; ++b)
@@ -959,37 +1093,18 @@ void Engine::encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, f
   // NULL selects the model's own stream, ordered after and before the legacy
   // null stream so that NULL behaves like the default stream for the caller.
   hipStream_t st = stream ? stream : stream_;
-  BatchPlan p;
-  p.B = B;
-  p.seq_start.resize(static_cast<size_t>(B));
-  p.q_len.resize(static_cast<size_t>(B));
-  p.k_len.resize(static_cast<size_t>(B));
-  int64_t T = 0;
-  for (int b = 0; b < B; ++b) {
-    const int n = h_lens[b];
-    if (n < 0 || n > max_len_) fail("sequence length outside [0, max_len]");
-    p.seq_start[static_cast<size_t>(b)] = static_cast<int32_t>(T);
-    p.q_len[static_cast<size_t>(b)] = n;
-    p.k_len[static_cast<size_t>(b)] = n;
-    p.max_q = std::max(p.max_q, n);
-    T += n;
-  }
-  if (T > (int64_t{1} << 30)) fail("batch too large");
-  p.T = static_cast<int>(T);
-  p.L = p.max_q;
+  BatchPlan p = plan_lens(h_lens, B);
   if (p.T == 0) return;
-  set_order(p);
-  ensure_workspace(p.T, B);
-  // The staging buffer is reused by the next call: make sure the previous
-  // upload from it has been consumed before overwriting.
-  hip_check(hipStreamSynchronize(st), "encode_device: previous upload");
+  ensure_workspace(p.Tb, p.Bb);
+  begin_call(st);
   if (!stream) {
     if (!ev_null_) hip_check(hipEventCreateWithFlags(&ev_null_, hipEventDisableTiming), "event");
     hip_check(hipEventRecord(ev_null_, nullptr), "record null stream");
     hip_check(hipStreamWaitEvent(st, ev_null_, 0), "wait null stream");
   }
-  upload_batch(p, nullptr, nullptr, st);
+  set_seq_table(p, h_lens, ws_.seq, st);
   run_device_maybe_graph(p, d_ids, d_hidden, false, st);
+  end_call(st);
   if (!stream) {
     hip_check(hipEventRecord(ev_null_, st), "record model stream");
     hip_check(hipStreamWaitEvent(nullptr, ev_null_, 0), "null stream waits");
@@ -1013,9 +1128,10 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     if (qtype[b] < 0 || qtype[b] > 2) fail("qtype must be 0, 1 or 2");
     qt[static_cast<size_t>(b)] = static_cast<int32_t>(qtype[b]);
   }
-  ensure_workspace(std::max(p.T, 1), B);
+  ensure_workspace(p.Tb, p.Bb);
   const int D = D_;
   hipStream_t st = stream_;
+  begin_call(st);
   if (p.T > 0) {
     upload_batch(p, packed.data(), qt.data(), st);
     run_device_maybe_graph(p, ids_.as<int32_t>(), X_.as<float>(), true, st);
@@ -1082,7 +1198,7 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     g.out_dtype = DT_F32;
     g.bias = sc_b1_.as<float>();
     g.act = 1;
-    gemm("scorer_linear1", g, st);
+    gemm("scorer_linear1", g, ws_, st);
     GemmArgs g2 = g;
     g2.A = tail_s1_.get();
     g2.W = sc_w2_.get();
@@ -1091,7 +1207,7 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     g2.ldo = 1;
     g2.bias = sc_b2_.as<float>();
     g2.act = 0;
-    gemm("scorer_linear2", g2, st);
+    gemm("scorer_linear2", g2, ws_, st);
   }
   launch_act_features(tail_s2_.as<float>(), tail_idx_.as<int32_t>() + nrow, B, K,
                       tail_rows_.as<float>() + static_cast<size_t>(nmk) * D, D, D,
@@ -1112,7 +1228,7 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     g.out_dtype = DT_F32;
     g.bias = act_b1_.as<float>();
     g.act = 1;
-    gemm("act_linear1", g, st);
+    gemm("act_linear1", g, ws_, st);
     GemmArgs g2 = g;
     g2.A = tail_ah_.get();
     g2.lda = 256;
@@ -1124,7 +1240,7 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     g2.ldo = n_act_;
     g2.bias = act_b2_.as<float>();
     g2.act = 0;
-    gemm("act_linear2", g2, st);
+    gemm("act_linear2", g2, ws_, st);
   }
   launch_act_softmax(tail_ao_.as<float>(), B, n_act_, tail_act_.as<float>(), st);
   hip_check(hipMemcpyAsync(logits, tail_lg_.get(), static_cast<size_t>(nmk) * 4, hipMemcpyDeviceToHost, st),
@@ -1132,6 +1248,7 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
   hip_check(hipMemcpyAsync(act, tail_act_.get(), static_cast<size_t>(B) * n_act_ * 4,
                            hipMemcpyDeviceToHost, st),
             "download act");
+  end_call(st);
   hip_check(hipStreamSynchronize(st), "forward: decision head");
   if (profile_) prof_collect();
 }

@@ -1,7 +1,9 @@
 // engine.hpp -- the device-resident DecisionModel (host orchestration).
 //
 // Owns the device copies of all weights, a grow-only workspace, one HIP stream
-// (default priority) and a cache of captured hipGraphs keyed by batch shape.
+// (default priority) and a cache of captured hipGraphs keyed by a shape
+// bucket: every kernel reads the real token count and the per-sequence
+// lengths from a device table, so one graph serves all batches of a bucket.
 // The forward follows src/model.cpp:309-536 op for op; the differences are in
 // layout only:
 //   * tokens are packed: sequence b occupies rows [seq_start[b],
@@ -72,11 +74,28 @@ class PinnedBuf {
   size_t bytes_ = 0;
 };
 
-// Device-side batch layout (see the file comment).
+// Device-side batch layout (see the file comment).  B, T and max_q are the
+// batch's own; Bb, Tb and max_qb its bucket, which sizes the launches (and
+// keys the graph cache): Bb the next power of two of B, Tb the token count
+// rounded up (to 64 up to 1024 tokens, then to an eighth of its power of
+// two), max_qb the longest row rounded up to the attention query block (128,
+// or 1024 above 1024).
 struct BatchPlan {
   int B = 0, L = 0, T = 0, max_q = 0;
+  int Bb = 0, Tb = 0, max_qb = 0;
   std::vector<int32_t> seq_start, q_len, k_len;
   std::vector<int32_t> order;  // sequences by decreasing length (attention dispatch order)
+};
+
+// Device buffers one forward works in (the engine's grow-only workspace).
+struct Ws {
+  int32_t* seq = nullptr;  // sequence table (sjh_kernels.hpp, seq_table_ints(Bb) ints)
+  int* tok_pos = nullptr;  // [Tb] position of each token in its sequence
+  int* tok_seq = nullptr;  // [Tb] sequence of each token
+  void *Y = nullptr, *QKV = nullptr, *O = nullptr, *G = nullptr;
+  float* Z = nullptr;  // LoRA [Tb, r]
+  float* partial = nullptr;  // split-K partial sums
+  int64_t partial_cap = 0;   // floats
 };
 
 class Engine {
@@ -97,6 +116,7 @@ class Engine {
                      hipStream_t stream);
 
   void set_profile(bool on);
+  void graph_stats(int32_t* cached, int64_t* captures, int64_t* replays);
   std::vector<std::tuple<const char*, double, int64_t>> profile_totals();
 
  private:
@@ -111,29 +131,41 @@ class Engine {
   };
   struct Graph {
     hipGraphExec_t exec = nullptr;
+    uint64_t last_use = 0;  // LRU eviction
   };
+  static constexpr size_t kMaxGraphs = 32;
 
   void stage_weights(const sjh_model_desc& d);
   BatchPlan plan(const int64_t* ids, const int64_t* mask, int B, int L, int32_t* ids_out) const;
-  void ensure_workspace(int T, int B);
+  BatchPlan plan_lens(const int32_t* h_lens, int B) const;
+  void ensure_workspace(int Tb, int Bb);
+  // the sequence table (and the token ids) through the pinned staging buffer
   void upload_batch(const BatchPlan& p, const int32_t* h_ids, const int32_t* h_qtype,
                     hipStream_t st);
+  // the sequence table of a device-resident batch: built by a kernel from
+  // the lengths in its arguments (up to kSeqTableMaxB sequences), else uploaded
+  void set_seq_table(const BatchPlan& p, const int32_t* h_lens, int32_t* table, hipStream_t st);
   // device work from token ids to the final hidden states in X (and, with
   // `head`, through the decision-head layers)
-  void run_device(const BatchPlan& p, const int32_t* d_ids, float* X, bool head,
+  void run_device(const BatchPlan& p, const Ws& w, const int32_t* d_ids, float* X, bool head,
                   hipStream_t st);
   void run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, float* X, bool head,
                               hipStream_t st);
-  void enqueue_encoder(const BatchPlan& p, const int32_t* d_ids, float* X, hipStream_t st);
-  void enqueue_head_layers(const BatchPlan& p, float* X, hipStream_t st);
+  void enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_ids, float* X,
+                       hipStream_t st);
+  void enqueue_head_layers(const BatchPlan& p, const Ws& w, float* X, hipStream_t st);
+  // order this call's stream after the engine's previous call (any stream),
+  // and mark the end of this call's work
+  void begin_call(hipStream_t st);
+  void end_call(hipStream_t st);
 
   // launch helpers (record profile events when enabled)
-  void gemm(const char* name, const GemmArgs& g, hipStream_t st);
+  void gemm(const char* name, const GemmArgs& g, const Ws& w, hipStream_t st);
   void ln(const char* name, const LnArgs& a, hipStream_t st);
   // X += A . W^T followed by the layer norm `a` that reads X: for short
   // batches the split-K residual epilogue is folded into that layer norm.
   void resid_gemm_ln(const char* gname, const GemmArgs& g, const char* lname, LnArgs a,
-                     hipStream_t st);
+                     const Ws& w, hipStream_t st);
   void attn(const char* name, const AttnArgs& a, hipStream_t st);
   void prof_begin(hipStream_t st);
   void prof_end(const char* name, hipStream_t st);
@@ -161,6 +193,7 @@ class Engine {
   DevBuf ids_, seqinfo_, tok_pos_, tok_seq_;
   DevBuf X_, Y_, QKV_, O_, G_, Z_;
   DevBuf splitk_;  // split-K partial sums for short batches (GemmArgs::partial)
+  Ws ws_;          // views of the buffers above
   DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_lg_, tail_ain_, tail_ah_,
       tail_ao_, tail_act_;
   PinnedBuf h_stage_, h_out_;
@@ -168,7 +201,14 @@ class Engine {
 
   hipStream_t stream_ = nullptr;
   hipEvent_t ev_null_ = nullptr;  // orders NULL-stream callers of encode_device
+  // ev_done_: the end of the last call's device work, on whichever stream it
+  // ran; every call waits for it first.  ev_upload_: the last copy out of
+  // the pinned staging buffer, awaited before the buffer is rewritten.
+  hipEvent_t ev_done_ = nullptr, ev_upload_ = nullptr;
+  bool done_recorded_ = false, upload_recorded_ = false;
   std::map<std::vector<int64_t>, Graph> graphs_;
+  uint64_t graph_clock_ = 0;
+  int64_t n_captures_ = 0, n_replays_ = 0;
   std::mutex mu_;
 
   bool profile_ = false;

@@ -145,6 +145,14 @@ __device__ __forceinline__ void consume(const T& v) {
   asm volatile("" ::"v"(v));
 }
 
+// The arguments a kernel works with: M becomes the device row count when
+// the launch carries one (GemmArgs::M_dev).
+__device__ __forceinline__ GemmArgs resolve_rows(const GemmArgs& g0) {
+  GemmArgs g = g0;
+  if (g.M_dev) g.M = *g.M_dev;
+  return g;
+}
+
 // Epilogue on the accumulators in registers (see the comment above).
 // TAB_LDS: the RoPE table rows of the tile are staged in LDS at rope_tab
 // (given whenever the tile has rotated columns).
@@ -365,8 +373,9 @@ __device__ void splitk_output(const GemmArgs& g, int S, int m, int n);
 
 template <int BM, int BN, int WGM, int WGN, int NS, int BK, int EPI, typename OutT,
           bool SPLITK = false>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs g) {
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs g0) {
   using TT = DTile<BM, BN, WGM, WGN, NS, BK>;
+  const GemmArgs g = resolve_rows(g0);
   constexpr int TI = TT::TI, TJ = TT::TJ, G = TT::G, RB = TT::RB, CPR = TT::CPR;
   constexpr int KS = BK / 16;  // MFMA K steps per stage
   extern __shared__ __attribute__((aligned(16))) char dsmem[];
@@ -375,6 +384,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs 
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
   const int tile_m = tile / tiles_n, tile_n = tile - tile_m * tiles_n;
   const int m0 = tile_m * BM;
+  if (m0 >= g.M) return;  // a row tile past the device row count (uniform)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
   const int l32 = lane & 31, hb = lane >> 5;
@@ -482,7 +492,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs 
     // splitk_epilogue_kernel adds the splits in order and applies the
     // epilogue.  The tile holds every W row its outputs need (GEGLU input and
     // gate rows, both halves of a RoPE head).
-    float* part = g.partial + static_cast<int64_t>(blockIdx.y) * g.M * g.n_w;
+    float* part = g.partial + static_cast<int64_t>(blockIdx.y) * g.part_rows * g.n_w;
     const int row_base = m0 + wm * TT::WM + 4 * hb;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -726,8 +736,10 @@ constexpr int pers_waves_per_simd() {
 
 template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8, int EPI, typename OutT>
 __global__ __launch_bounds__(64 * WGM * WGN, (pers_waves_per_simd<BM, BN, WGM, WGN, NS, BK, W8>()))
-void gemm_bf16_pers_kernel(GemmArgs g) {
+void gemm_bf16_pers_kernel(GemmArgs g0) {
   using TT = PTile<BM, BN, WGM, WGN, NS, BK, W8>;
+  const GemmArgs g = resolve_rows(g0);
+  if (g.M <= 0) return;
   constexpr int TI = TT::TI, TJ = TT::TJ, G = TT::G, NW = TT::NW;
   constexpr int RBA = TT::RBA, RBW = TT::RBW;
   constexpr int KS = BK / 16;  // MFMA K steps per stage
@@ -1200,7 +1212,7 @@ void launch_mfma(const GemmArgs& g, hipStream_t st) {
 // visible to the epilogue, whichever XCD wrote them.
 __device__ __forceinline__ float splitk_sum(const GemmArgs& g, int S, int m, int col) {
   float v = 0.f;
-  for (int sp = 0; sp < S; ++sp) v += g.partial[(static_cast<int64_t>(sp) * g.M + m) * g.n_w + col];
+  for (int sp = 0; sp < S; ++sp) v += g.partial[(static_cast<int64_t>(sp) * g.part_rows + m) * g.n_w + col];
   return v;
 }
 
@@ -1242,7 +1254,8 @@ __device__ void splitk_output(const GemmArgs& g, int S, int m, int n) {
 }
 
 template <typename OutT>
-__global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g, int S) {
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs g0, int S) {
+  const GemmArgs g = resolve_rows(g0);
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= static_cast<int64_t>(g.M) * g.N) return;
   const int m = static_cast<int>(idx / g.N);
@@ -1266,6 +1279,7 @@ void launch_splitk_epi(const GemmArgs& g, dim3 grid, hipStream_t st) {
 // short to split.
 int launch_splitk_partials(GemmArgs& g, hipStream_t st) {
   g.n_w = g.epi == EPI_GEGLU ? 2 * g.N : g.N;
+  g.part_rows = g.M;
   if (g.epi == EPI_GEGLU && g.N % (kSkBN / 2) != 0) return 0;
   const int tiles_n = g.epi == EPI_GEGLU ? g.N / (kSkBN / 2) : (g.N + kSkBN - 1) / kSkBN;
   const int tiles = ((g.M + kSkBM - 1) / kSkBM) * tiles_n;
@@ -1308,7 +1322,8 @@ constexpr int gBM = 64, gBN = 64, gBK = 16;
 constexpr int gLdc = gBN + 4;
 
 template <typename InT, typename OutT>
-__global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs g0) {
+  const GemmArgs g = resolve_rows(g0);
   constexpr int kStage = 2 * gBK * (gBM + 1);  // As[k][m] and Ws[k][n]
   constexpr int kFloats = kStage > gBM * gLdc ? kStage : gBM * gLdc;
   __shared__ float smem[kFloats];
@@ -1317,6 +1332,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs g) {
 
   const int tile_n = blockIdx.x, tile_m = blockIdx.y;
   const int m0 = tile_m * gBM;
+  if (m0 >= g.M) return;  // uniform
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const InT* A = static_cast<const InT*>(g.A);
   const InT* W = static_cast<const InT*>(g.W);

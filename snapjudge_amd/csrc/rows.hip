@@ -25,12 +25,14 @@ template <int NPL, typename InT, typename ResT, typename OutT>
 __global__ __launch_bounds__(64 * kLnWaves) void ln_rows_kernel(LnArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
-  if (r >= a.M) return;
+  if (r >= (a.M_dev ? *a.M_dev : a.M)) return;
   const int D = a.D;
   const int64_t src_row = a.ids ? static_cast<int64_t>(a.ids[r]) : static_cast<int64_t>(r);
   const InT* in = static_cast<const InT*>(a.in) + src_row * a.ld_in;
   const ResT* res = a.resid ? static_cast<const ResT*>(a.resid) + static_cast<int64_t>(r) * a.ld_in
                             : nullptr;
+  const float* add = a.add ? a.add + static_cast<int64_t>(min(max(a.add_ids[r], 0), a.add_rows - 1)) * a.ld_add
+                           : nullptr;
   float v[NPL];
   const int npl = (D + 63) >> 6;
   double s = 0.0;
@@ -41,6 +43,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_rows_kernel(LnArgs a) {
       float x = 0.f;
       if (j < D) {
         x = load_f32(in + j);
+        if (add) x += add[j];
         if (res) x += load_f32(res + j);
       }
       v[i] = x;
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
   const int lane = threadIdx.x & 63;
   // The row is uniform over the wave: scalar row addresses and gather index.
   const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * kLnWaves + (threadIdx.x >> 6));
-  if (r >= a.M) return;
+  if (r >= (a.M_dev ? *a.M_dev : a.M)) return;
   const int D = a.D, nch = D >> 2;
   const int64_t src_row = a.ids ? static_cast<int64_t>(a.ids[r]) : static_cast<int64_t>(r);
   const InT* in = static_cast<const InT*>(a.in) + src_row * a.ld_in;
@@ -202,9 +205,23 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
 #pragma unroll
   for (int i = 0; i < NV; ++i)
     if (FULL || lane + 64 * i < nch) vr[i] = Vec4<InT>::raw(in + 4 * (lane + 64 * i));
+  // the added row (a learned position embedding), when given
+  f32x4_t ar[NV] = {};
+  if (a.add) {
+    const float* add = a.add + static_cast<int64_t>(min(max(a.add_ids[r], 0), a.add_rows - 1)) * a.ld_add;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (FULL || lane + 64 * i < nch) ar[i] = *reinterpret_cast<const f32x4_t*>(add + 4 * (lane + 64 * i));
+  }
   float v[NV][4];
 #pragma unroll
   for (int i = 0; i < NV; ++i) Vec4<InT>::cvt(vr[i], v[i]);
+  if (a.add) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[i][k] += ar[i][k];
+  }
   if constexpr (kParts) {
     // x = in + (p_0 + p_1 + ... + p_{S-1} + bias), summed from 0 in split
     // order: the split-K residual epilogue's arithmetic
@@ -385,9 +402,10 @@ __global__ void token_index_kernel(const int* seq_start, const int* rows, int* t
 }
 
 __global__ void add_row_embedding_kernel(float* X, int64_t ldx, const float* table,
-                                         const int* sel, const int* tok_seq, int T, int D) {
+                                         const int* sel, const int* tok_seq, int T,
+                                         const int* T_dev, int D) {
   const int t = blockIdx.x;
-  if (t >= T) return;
+  if (t >= (T_dev ? *T_dev : T)) return;
   const float* te = table + static_cast<int64_t>(sel[tok_seq[t]]) * D;
   float* x = X + static_cast<int64_t>(t) * ldx;
   for (int j = threadIdx.x; j < D; j += blockDim.x) x[j] += te[j];
@@ -458,7 +476,76 @@ __global__ void act_softmax_kernel(const float* a, int B, int n, float* act) {
     act[static_cast<int64_t>(b) * n + j] = static_cast<float>(static_cast<double>(expf(ab[j] - amx)) / as);
 }
 
+// Lengths of a batch, passed by value (no host staging buffer).
+struct SeqTableArgs {
+  int B, Bb;
+  int32_t lens[kSeqTableMaxB];
+};
+
+// The per-batch sequence table (layout in sjh_kernels.hpp) from the lengths,
+// one workgroup of kSeqTableMaxB threads, thread b = table entry b.  The
+// order is the stable sort by decreasing length: entry b's rank counts the
+// longer entries and the equal ones before it.
+__global__ __launch_bounds__(kSeqTableMaxB) void seq_table_kernel(SeqTableArgs a, int32_t* t) {
+  __shared__ int32_t len_s[kSeqTableMaxB], start_s[kSeqTableMaxB];
+  const int b = threadIdx.x;
+  const int32_t* lens = a.lens;
+  const int n = b < a.B ? lens[b] : 0;
+  len_s[b] = n;
+  __syncthreads();
+  // exclusive prefix sum of the lengths (Hillis-Steele over the workgroup)
+  int incl = n;
+  start_s[b] = incl;
+  __syncthreads();
+  for (int off = 1; off < kSeqTableMaxB; off <<= 1) {
+    const int add = b >= off ? start_s[b - off] : 0;
+    __syncthreads();
+    incl += add;
+    start_s[b] = incl;
+    __syncthreads();
+  }
+  const int total = start_s[kSeqTableMaxB - 1];
+  const int start = b < a.B ? incl - n : total;
+  if (b == 0) {
+    t[0] = total;
+    t[1] = a.B;
+    t[2] = 0;
+    t[3] = 0;
+  }
+  if (b >= a.Bb) return;
+  int rank = b;  // empty entries keep their place after the real sequences
+  if (b < a.B) {
+    rank = 0;
+    for (int c = 0; c < a.B; ++c) {
+      const int m = len_s[c];
+      rank += (m > n || (m == n && c < b)) ? 1 : 0;
+    }
+  }
+  int32_t* seq_start = t + kSeqHdr;
+  seq_start[b] = start;
+  seq_start[a.Bb + b] = n;       // q_len
+  seq_start[2 * a.Bb + b] = n;   // k_len
+  seq_start[3 * a.Bb + b] = 0;   // qtype
+  seq_start[4 * a.Bb + rank] = b;  // order
+  int32_t* meta = t + (kSeqHdr + 5 * a.Bb + 3) / 4 * 4 + 4 * rank;
+  meta[0] = start;
+  meta[1] = n;
+  meta[2] = n;
+  meta[3] = 0;
+}
+
 }  // namespace
+
+void launch_seq_table(const int32_t* h_lens, int B, int Bb, int32_t* table, hipStream_t st) {
+  require(B >= 0 && B <= Bb && Bb <= kSeqTableMaxB, "seq_table: need 0 <= B <= Bb <= 256");
+  require(B == 0 || h_lens != nullptr, "seq_table: null lengths");
+  SeqTableArgs a;
+  a.B = B;
+  a.Bb = Bb;
+  for (int b = 0; b < kSeqTableMaxB; ++b) a.lens[b] = b < B ? h_lens[b] : 0;
+  seq_table_kernel<<<1, kSeqTableMaxB, 0, st>>>(a, table);
+  check_launch("seq_table");
+}
 
 void launch_act_features(const float* s2, const int* mmask, int B, int K, const float* cls,
                          int64_t ld_cls, int D, float* logits, float* ain, int64_t ld_ain,
@@ -474,6 +561,28 @@ void launch_act_softmax(const float* a, int B, int n, float* act, hipStream_t st
   check_launch("act_softmax");
 }
 
+namespace {
+bool ln_aligned(const void* p, int dt) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) & (dt == DT_BF16 ? 7u : 15u)) == 0;
+}
+
+// The vector kernel's shape: 4-column chunks, every row start 16-byte (fp32)
+// or 8-byte (bf16) aligned, at most 1024 columns.
+bool ln_vec_ok(const LnArgs& a) {
+  return a.D % 4 == 0 && a.D <= 1024 && a.ld_in % 4 == 0 && a.ld_x % 4 == 0 &&
+         a.ld_y % 4 == 0 && a.ld_add % 4 == 0 && ln_aligned(a.in, a.in_dtype) &&
+         ln_aligned(a.resid, a.resid_dtype) && ln_aligned(a.xio, DT_F32) &&
+         ln_aligned(a.x_out, DT_F32) && ln_aligned(a.y_out, a.y_dtype) &&
+         ln_aligned(a.w, DT_F32) && ln_aligned(a.b, DT_F32) && ln_aligned(a.add, DT_F32);
+}
+}  // namespace
+
+bool ln_takes_parts(const LnArgs& a) {
+  return ln_vec_ok(a) && a.resid == nullptr && a.add == nullptr && a.in_dtype == DT_F32 &&
+         a.ids == nullptr && a.xio != nullptr && ln_aligned(a.parts, DT_F32) &&
+         a.part_stride % 4 == 0 && a.ld_part % 4 == 0 && ln_aligned(a.part_bias, DT_F32);
+}
+
 void launch_ln(const LnArgs& a, hipStream_t st) {
   if (a.M <= 0) return;
   require(a.D > 0 && a.D <= 64 * kLnMaxPerLane, "layer_norm: D must be in [1, 4096]");
@@ -483,18 +592,11 @@ void launch_ln(const LnArgs& a, hipStream_t st) {
         "layer_norm: residual write-back needs fp32 rows without a gather");
   require(!a.x_out || a.ld_x >= a.D, "layer_norm: ld_x < D");
   require(!a.y_out || a.ld_y >= a.D, "layer_norm: ld_y < D");
-  // vector path: 4-column chunks, every row start 16-byte (fp32) / 8-byte (bf16) aligned
-  auto al = [](const void* p, int dt) {
-    return p == nullptr || (reinterpret_cast<uintptr_t>(p) & (dt == DT_BF16 ? 7u : 15u)) == 0;
-  };
-  const bool vec = a.D % 4 == 0 && a.D <= 1024 && a.ld_in % 4 == 0 && a.ld_x % 4 == 0 &&
-                   a.ld_y % 4 == 0 && al(a.in, a.in_dtype) && al(a.resid, a.resid_dtype) &&
-                   al(a.xio, DT_F32) && al(a.x_out, DT_F32) && al(a.y_out, a.y_dtype) &&
-                   al(a.w, DT_F32) && al(a.b, DT_F32);
+  require(!a.add || (a.add_ids && a.add_rows > 0 && a.ld_add >= a.D),
+          "layer_norm: an added row needs its row indices, a row count and ld_add >= D");
+  const bool vec = ln_vec_ok(a);
   if (a.n_parts > 0) {
-    require(vec && a.resid == nullptr && a.in_dtype == DT_F32 && a.ids == nullptr && a.xio &&
-                a.parts && al(a.parts, DT_F32) && a.part_stride % 4 == 0 && a.ld_part % 4 == 0 &&
-                al(a.part_bias, DT_F32),
+    require(a.parts && ln_takes_parts(a),
             "layer_norm: split-K partials need fp32 vector rows written back to xio");
     ln_vec_dispatch<float, PartsRes>(a, st);
   } else if (vec && a.resid == nullptr) {
@@ -536,9 +638,9 @@ void launch_token_index(const int* seq_start, const int* rows, int B, int* tok_p
 }
 
 void launch_add_row_embedding(float* X, int64_t ldx, const float* table, const int* sel,
-                              const int* tok_seq, int T, int D, hipStream_t st) {
+                              const int* tok_seq, int T, const int* T_dev, int D, hipStream_t st) {
   if (T <= 0) return;
-  add_row_embedding_kernel<<<T, 256, 0, st>>>(X, ldx, table, sel, tok_seq, T, D);
+  add_row_embedding_kernel<<<T, 256, 0, st>>>(X, ldx, table, sel, tok_seq, T, T_dev, D);
   check_launch("add_row_embedding");
 }
 

@@ -27,7 +27,12 @@ struct GemmArgs {
   int64_t lda = 0;
   const void* W = nullptr;
   int64_t ldw = 0;
+  // M sizes the launch (grid, tile choice, split-K strides).  With M_dev set,
+  // the kernels read the real row count (<= M) from device memory at start
+  // and touch rows [0, *M_dev) only: one launch, or one captured graph,
+  // then serves every row count up to M.
   int M = 0, N = 0, K = 0;
+  const int* M_dev = nullptr;
   int in_dtype = DT_BF16;  // A (and W unless w_dtype says otherwise)
   // DT_FP8: W holds e4m3 codes and row n of W stands for code * w_scale[n]
   // (A stays bf16); the scale multiplies the fp32 accumulator.
@@ -55,13 +60,14 @@ struct GemmArgs {
   // set by the launcher for split-K launches
   int k_chunk = 0;  // K steps (of the MFMA K depth) per split
   int n_w = 0;      // rows of W (= N, or 2F for GEGLU)
+  int part_rows = 0;  // the launch's M: split s of row m sits at partial[(s * part_rows + m) * n_w]
 };
 void launch_gemm(const GemmArgs& g, hipStream_t st);
 // Short batches (M <= 256) of a residual GEMM (EPI_RESID, bf16 MFMA path):
 // launches only the split-K product into g.partial and returns the number of
 // splits S >= 2; the caller then adds the splits with the layer norm that
-// reads X next (LnArgs::parts).  Returns 0, having launched nothing, when the
-// split-K path does not apply.
+// reads X next (LnArgs::parts), which must then satisfy ln_takes_parts.
+// Returns 0, having launched nothing, when the split-K path does not apply.
 int launch_gemm_resid_partials(const GemmArgs& g, hipStream_t st);
 
 // Row LayerNorm over [M, D] rows (src/tensor.cpp:54-79 semantics).
@@ -94,8 +100,20 @@ struct LnArgs {
   int y_dtype = DT_BF16;
   int64_t ld_y = 0;
   int M = 0, D = 0;
+  const int* M_dev = nullptr;  // as GemmArgs::M_dev: rows [0, *M_dev) of the M launched
+  // optional second input row added to the first, before the residual:
+  // x = in_row + add[add_ids[r] clamped to [0, add_rows)] (fp32 rows, ld_add),
+  // the learned position embedding of a BERT-style encoder
+  const float* add = nullptr;
+  const int* add_ids = nullptr;
+  int add_rows = 0;
+  int64_t ld_add = 0;
 };
 void launch_ln(const LnArgs& a, hipStream_t st);
+// Whether launch_ln accepts a.n_parts > 0 (split-K partials folded into the
+// residual) for rows of this shape: the vector kernel's D % 4 == 0 and
+// D <= 1024 with 16-byte aligned fp32 rows.
+bool ln_takes_parts(const LnArgs& a);
 
 // Non-causal attention over a varlen batch.  Sequence b owns rows
 // [seq_start[b], seq_start[b] + max(q_len[b], k_len[b])); its queries are the
@@ -137,9 +155,26 @@ void launch_rope(void* qkv, int dtype, int64_t M, int64_t ld, const int* pos, in
 void launch_token_index(const int* seq_start, const int* rows, int B, int* tok_pos,
                         int* tok_seq, hipStream_t st);
 
-// X[t, :] += table[sel[tok_seq[t]], :] for t < T (type embedding of a row's qtype).
+// X[t, :] += table[sel[tok_seq[t]], :] for t < T (type embedding of a row's
+// qtype); with T_dev, for t < *T_dev (<= T).
 void launch_add_row_embedding(float* X, int64_t ldx, const float* table, const int* sel,
-                              const int* tok_seq, int T, int D, hipStream_t st);
+                              const int* tok_seq, int T, const int* T_dev, int D, hipStream_t st);
+
+// Per-batch sequence table (device int32), for Bb >= B table entries:
+//   [0] total tokens T = sum of lens, [1] B, [2..3] 0,
+//   seq_start[Bb] at 4, q_len[Bb], k_len[Bb], qtype[Bb], order[Bb], then,
+//   16-byte aligned at seq_table_meta(Bb), meta[4 * Bb] = {seq_start, q_len,
+//   k_len, 0} of order[z] for z < Bb.
+// Entries b >= B are empty sequences (start T, length 0) that every kernel
+// skips; order lists the real sequences longest first (stable), then the
+// empty ones.
+constexpr int kSeqHdr = 4;
+inline size_t seq_table_meta(int Bb) { return (static_cast<size_t>(kSeqHdr) + 5u * Bb + 3) / 4 * 4; }
+inline size_t seq_table_ints(int Bb) { return seq_table_meta(Bb) + 4u * Bb; }
+// Builds that table on the device from lengths passed by value in the kernel
+// arguments (no host staging buffer): q_len = k_len = lens[b], qtype 0.
+constexpr int kSeqTableMaxB = 256;
+void launch_seq_table(const int32_t* h_lens, int B, int Bb, int32_t* table, hipStream_t st);
 
 // dst[i, :] = idx[i] >= 0 ? src[idx[i], :] : 0   (fp32 rows)
 void launch_gather_rows(const float* src, int64_t ld_src, const int* idx, int n, int D,

@@ -10,6 +10,11 @@ anywhere, so the CPU reference (which widens BF16 to fp32 on load,
 src/safetensors.cpp:109-135) and the GPU see identical values.
 
 Presets are the five configurations of BASELINE.json.
+
+SjModel checkpoints (snapjudge's own BERT-style model, src/sj_model.cpp:87-204)
+are ``sj_config.json`` + ``model.safetensors`` with the ``sj.*`` tensor names;
+make_sj_model draws their norm gains and every bias at random too, so that a
+dropped bias or a swapped norm shows in parity.
 """
 from __future__ import annotations
 
@@ -141,30 +146,98 @@ def flat_cfg(rl: dict, enc: dict) -> dict:
 _DT = {"F32": (np.float32, 4), "F16": (np.float16, 2), "BF16": (np.uint16, 2)}
 
 
-def write_checkpoint(path: str, rl: dict, enc: dict, tensors: dict, store: str = "F32") -> None:
+def write_safetensors(path: str, tensors: dict, store="F32") -> None:
+    """Write a .safetensors file.  ``store`` is one dtype for every tensor
+    ("F32", "F16", "BF16") or a function name -> dtype; a tensor given as
+    (dtype, raw ndarray) is written as is (e.g. ("F8_E4M3", uint8 codes))."""
+    header, blobs, off = {}, [], 0
+    for k, v in tensors.items():
+        if isinstance(v, tuple):
+            dt, arr = v
+            raw = np.ascontiguousarray(arr).tobytes()
+            shape = list(arr.shape)
+        else:
+            dt = store(k) if callable(store) else store
+            if dt == "BF16":
+                raw = bf16_bits(v).tobytes()
+            elif dt == "F16":
+                raw = v.astype(np.float16).tobytes()
+            else:
+                raw = np.ascontiguousarray(v, dtype=np.float32).tobytes()
+            shape = list(v.shape)
+        header[k] = {"dtype": dt, "shape": shape, "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    hj = json.dumps(header).encode()
+    hj += b" " * ((8 - len(hj) % 8) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(hj)))
+        f.write(hj)
+        for b in blobs:
+            f.write(b)
+
+
+def write_checkpoint(path: str, rl: dict, enc: dict, tensors: dict, store="F32") -> None:
     os.makedirs(os.path.join(path, "encoder"), exist_ok=True)
     with open(os.path.join(path, "rl_agent_config.json"), "w") as f:
         json.dump(rl, f, indent=1)
     with open(os.path.join(path, "encoder", "config.json"), "w") as f:
         json.dump(enc, f, indent=1)
-    header, blobs, off = {}, [], 0
-    for k, v in tensors.items():
-        if store == "BF16":
-            raw = bf16_bits(v).tobytes()
-        elif store == "F16":
-            raw = v.astype(np.float16).tobytes()
-        else:
-            raw = np.ascontiguousarray(v, dtype=np.float32).tobytes()
-        header[k] = {"dtype": store, "shape": list(v.shape), "data_offsets": [off, off + len(raw)]}
-        blobs.append(raw)
-        off += len(raw)
-    hj = json.dumps(header).encode()
-    hj += b" " * ((8 - len(hj) % 8) % 8)
-    with open(os.path.join(path, "model.safetensors"), "wb") as f:
-        f.write(struct.pack("<Q", len(hj)))
-        f.write(hj)
-        for b in blobs:
-            f.write(b)
+    write_safetensors(os.path.join(path, "model.safetensors"), tensors, store)
+
+
+# ---------------------------------------------------------------- SjModel
+def make_sj_model(hidden_size: int, num_layers: int, num_heads: int, vocab_size: int,
+                  intermediate_size: int | None = None, max_positions: int = 512,
+                  head_layers: int = 1, head_intermediate: int | None = None,
+                  norm_eps: float = 1e-5, std: float = 0.02, seed: int = 0, store: str = "F32"):
+    """(sj_config, tensors) of an SjModel (src/sj_model.cpp:87-204 names and
+    shapes), fp32 arrays (bf16-exact with store="BF16")."""
+    D, V = hidden_size, vocab_size
+    F = intermediate_size or 4 * D
+    HF = head_intermediate or 4 * D
+    rng = np.random.default_rng(seed)
+    rnd = bf16_round if store == "BF16" else (lambda a: a)
+
+    def n(*shape, scale=std, mean=0.0):
+        v = rng.standard_normal(int(np.prod(shape)), dtype=np.float32) * np.float32(scale)
+        return rnd((v + np.float32(mean)).reshape(shape))
+
+    t = {"sj.embeddings.word.weight": n(V, D), "sj.embeddings.position.weight": n(max_positions, D),
+         "sj.embeddings.norm.weight": n(D, scale=0.05, mean=1.0), "sj.embeddings.norm.bias": n(D)}
+
+    def layer(p, ff, n1="attn_norm", n2="ffn_norm"):
+        t[p + n1 + ".weight"], t[p + n1 + ".bias"] = n(D, scale=0.05, mean=1.0), n(D)
+        for x in "qkvo":
+            t[p + f"attn.{x}.weight"], t[p + f"attn.{x}.bias"] = n(D, D), n(D)
+        t[p + n2 + ".weight"], t[p + n2 + ".bias"] = n(D, scale=0.05, mean=1.0), n(D)
+        t[p + "ffn.w1.weight"], t[p + "ffn.w1.bias"] = n(ff, D), n(ff)
+        t[p + "ffn.w2.weight"], t[p + "ffn.w2.bias"] = n(D, ff), n(D)
+
+    for i in range(num_layers):
+        layer(f"sj.encoder.layers.{i}.", F)
+    t["sj.encoder.final_norm.weight"] = n(D, scale=0.05, mean=1.0)
+    t["sj.encoder.final_norm.bias"] = n(D)
+    t["sj.type_emb.weight"] = n(3, D)
+    for i in range(head_layers):
+        layer(f"sj.head.layers.{i}.", HF, "norm1", "norm2")
+    t["sj.scorer.norm.weight"], t["sj.scorer.norm.bias"] = n(D, scale=0.05, mean=1.0), n(D)
+    t["sj.scorer.w1.weight"], t["sj.scorer.w1.bias"] = n(D, D), n(D)
+    t["sj.scorer.w2.weight"], t["sj.scorer.w2.bias"] = n(1, D), n(1)
+    cfg = {"vocab_size": V, "hidden_size": D, "num_layers": num_layers, "num_heads": num_heads,
+           "intermediate_size": F, "max_positions": max_positions, "norm_eps": norm_eps,
+           "head_layers": head_layers, "head_intermediate": HF, "max_len": max_positions,
+           "head_max_len": 192, "n_types": 3, "cls_id": 1, "sep_id": 2, "mask_id": 4, "pad_id": 3}
+    return cfg, t
+
+
+def write_sj_checkpoint(path: str, cfg: dict, tensors: dict, store="F32") -> None:
+    """sj_config.json + model.safetensors, the layout SjModel checkpoints use
+    (src/sj_train.cpp:180-184)."""
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "sj_config.json"), "w") as f:
+        json.dump(cfg, f, indent=1)
+    write_safetensors(os.path.join(path, "model.safetensors"), tensors, store)
 
 
 def read_checkpoint(path: str):
@@ -208,6 +281,18 @@ def make_batch(B: int, L: int, lo: int, hi: int, vocab: int, seed: int = 0, pad_
         ids[b, :n] = rng.integers(0, vocab, size=n)
         mask[b, :n] = 1
     return ids, mask, lens.astype(np.int64)
+
+
+def batch_with_lens(lens, L: int, vocab: int, seed: int = 0, pad_id: int = 0):
+    """Right-padded ids [B, L] and mask for the given row lengths."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    ids = np.full((len(lens), L), pad_id, dtype=np.int64)
+    mask = np.zeros((len(lens), L), dtype=np.int64)
+    for b, n in enumerate(lens):
+        ids[b, :n] = rng.integers(0, vocab, size=n)
+        mask[b, :n] = 1
+    return ids, mask, lens
 
 
 def make_markers(lens, K: int, kinds, seed: int = 0):

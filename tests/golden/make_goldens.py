@@ -11,6 +11,11 @@ are committed, never weights.
                      {choice K=4, noul K=2}), hidden/logits/act
   cfg2_b1s128.npz    BASELINE config 2 (22 layers, D=768, bf16 weights), B=1,
                      S=128: encoder hidden states
+  cfg4_b4s8192.npz   BASELINE config 4 (the same 22-layer encoder, weights seed
+                     0, batch 4 x seq 8192, lengths U[4096, 8192] seed 1: the
+                     bench's batch): the shortest and the longest row, each run
+                     alone through all 22 layers (rows are independent,
+                     src/tensor.cpp:179-185), hidden states at sampled positions
 """
 import os
 import sys
@@ -64,6 +69,44 @@ def cfg2():
         hidden = ref.encode(ids, mask)
         print(f"cfg2 reference encode: {time.time() - t0:.1f} s")
     np.savez(os.path.join(HERE, "cfg2_b1s128.npz"), seed=seed, ids=ids, mask=mask, hidden=hidden)
+
+
+def cfg4_positions(n):
+    """Sampled positions of a row of length n: the first and last 16, and every
+    97th in between (every RoPE table region and the attention tile edges)."""
+    return np.unique(np.concatenate([np.arange(16), np.arange(n - 16, n),
+                                     np.arange(16, n - 16, 97)])).astype(np.int64)
+
+
+def _cfg4_row(args):
+    d, ids_row, threads = args
+    os.environ["SNAPJUDGE_THREADS"] = str(threads)
+    n = len(ids_row)
+    ref = RefModel(d)
+    t0 = time.time()
+    h = ref.encode(ids_row[None, :], np.ones((1, n), np.int64))[0]
+    print(f"cfg4 row n={n}: {time.time() - t0:.0f} s", flush=True)
+    return h[cfg4_positions(n)]
+
+
+def cfg4():
+    from multiprocessing import get_context
+
+    seed = 0
+    p = dict(synth.PRESETS["cfg4"])
+    rl, enc, w = synth.make_model(**p, seed=seed)
+    ids, _, lens = synth.make_batch(4, 8192, 4096, 8192, enc["vocab_size"], seed=1)
+    rows = [int(np.argmin(lens)), int(np.argmax(lens))]
+    with tempfile.TemporaryDirectory() as d:
+        synth.write_checkpoint(d, rl, enc, w, store=p["store"])
+        del w
+        jobs = [(d, ids[b, :lens[b]].copy(), 4) for b in rows]
+        with get_context("fork").Pool(len(jobs)) as pool:
+            outs = pool.map(_cfg4_row, jobs)
+    np.savez(os.path.join(HERE, "cfg4_b4s8192.npz"), seed=seed, batch_seed=1, rows=np.array(rows),
+             lens=lens, pos_short=cfg4_positions(int(lens[rows[0]])),
+             pos_long=cfg4_positions(int(lens[rows[1]])), hidden_short=outs[0],
+             hidden_long=outs[1])
 
 
 if __name__ == "__main__":

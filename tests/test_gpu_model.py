@@ -26,12 +26,19 @@ def valid_err(h, ref, mask):
     return float(np.abs(h[m] - ref[m]).max())
 
 
+# Calibration temperatures are clamped to [0.5, 5] (src/common.cpp:199-202);
+# T = 0.5 doubles logit differences before the softmax, so the 5e-3 bound is
+# checked at both ends of the range and at 1.
+TEMPERATURES = (0.5, 1.0, 5.0)
+
+
 def probs_err(orc, lg, lr, mm):
     e = 0.0
     for b in range(len(lg)):
         k = int(mm[b].sum())
-        e = max(e, float(np.abs(orc.calibrated_probs(lg[b, :k], 1.0) -
-                                orc.calibrated_probs(lr[b, :k], 1.0)).max()))
+        for t in TEMPERATURES:
+            e = max(e, float(np.abs(orc.calibrated_probs(lg[b, :k], t) -
+                                    orc.calibrated_probs(lr[b, :k], t)).max()))
     return e
 
 
@@ -172,7 +179,9 @@ def test_cfg3_shape_sampled_rows_and_batch_invariance(orc):
     h = m.encode(ids, mask)
     om = orc.model(w, cfg)
     order = np.argsort(lens)
-    for b in (order[0], order[1], order[32]):
+    # the two shortest, the median and the two longest rows (n near 512: four
+    # 128-query blocks, eight 64-key tiles per attention workgroup)
+    for b in (order[0], order[1], order[32], order[-2], order[-1]):
         n = int(lens[b])
         ref = om.encode(ids[b:b + 1, :n], mask[b:b + 1, :n])[0]
         err = float(np.abs(h[b, :n] - ref).max())
@@ -187,6 +196,96 @@ def test_cfg3_shape_sampled_rows_and_batch_invariance(orc):
     # reversing the batch order permutes the outputs and nothing else
     hr = m.encode(ids[::-1].copy(), mask[::-1].copy())
     assert np.array_equal(hr[::-1], h)
+    m.close()
+
+
+def test_graph_replay_serves_a_shape_bucket():
+    # Batches of different sizes, lengths and ids that fall in one shape
+    # bucket replay one captured graph; each result equals the same batch run
+    # launch by launch (bit for bit).  A batch in another bucket captures its
+    # own graph; coming back to the first bucket replays it again.
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg2"], num_hidden_layers=2), seed=41)
+    cfg = synth.flat_cfg(rl, enc)
+    g_on = sj.Model(w, cfg, precision=BF16, use_graphs=True)
+    g_off = sj.Model(w, cfg, precision=BF16, use_graphs=False)
+    # one bucket: 5..8 sequences (8 table entries), 1921..2048 tokens (an
+    # eighth of the octave above 1024), longest row 257..384 (three query blocks)
+    V = cfg["vocab_size"]
+    batches = [synth.batch_with_lens([384, 350, 330, 320, 300, 330], 384, V, seed=42),
+               synth.batch_with_lens([290, 300, 270, 260, 280, 300, 280], 320, V, seed=43),
+               synth.batch_with_lens([257, 250, 260, 240, 245, 255, 250, 265], 300, V, seed=44)]
+    for ids, mask, lens in batches:
+        assert 1920 < int(lens.sum()) <= 2048 and 256 < lens.max() <= 384
+    other = synth.batch_with_lens([200, 150, 60], 200, V, seed=45)
+    seen = []
+    for i, (ids, mask, lens) in enumerate(batches + [other, batches[0]]):
+        h = g_on.encode(ids, mask)
+        want = g_off.encode(ids, mask)
+        print(f"batch {i}: B={len(lens)} T={int(lens.sum())} graphs {g_on.graph_stats()}", flush=True)
+        assert np.array_equal(h, want)
+        seen.append(g_on.graph_stats())
+    assert seen[2] == {"cached": 1, "captures": 1, "replays": 2}
+    assert seen[3]["captures"] == 2 and seen[4] == {"cached": 2, "captures": 2, "replays": 3}
+    g_on.close()
+    g_off.close()
+
+
+def test_calls_on_two_streams_and_forward_are_ordered():
+    # encode_device calls on two streams and a forward() on the model's own
+    # stream share one workspace: each waits for the previous call.  Issued
+    # back to back with no host synchronization, every result equals the same
+    # call made alone.
+    import torch
+
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg2"], num_hidden_layers=2), seed=51)
+    cfg = synth.flat_cfg(rl, enc)
+    m = sj.Model(w, cfg, precision=BF16)
+    D = cfg["hidden_size"]
+    batches = [synth.make_batch(4, 256, 30 + 20 * i, 256, cfg["vocab_size"], seed=52 + i) for i in range(4)]
+    fwd_ids, fwd_mask, fwd_lens = synth.make_batch(3, 128, 20, 128, cfg["vocab_size"], seed=60)
+    mp, mm, qt = synth.make_markers(fwd_lens, 3, [(0, 3), (1, 3), (2, 2)], seed=60)
+    d_ids, d_out, want = [], [], []
+    for ids, mask, lens in batches:
+        packed = np.concatenate([ids[b, :lens[b]] for b in range(len(lens))]).astype(np.int32)
+        d_ids.append(torch.from_numpy(packed).cuda())
+        d_out.append(torch.full((len(packed), D), float("nan"), dtype=torch.float32, device="cuda"))
+        h = m.encode(ids, mask)
+        want.append(np.concatenate([h[b, :lens[b]] for b in range(len(lens))]))
+    lg_want, act_want = m.forward(fwd_ids, fwd_mask, mp, mm, qt)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]  # default priority
+    for rep in range(2):
+        for i, (ids, mask, lens) in enumerate(batches):
+            m.encode_device(d_ids[i].data_ptr(), lens.astype(np.int32), d_out[i].data_ptr(),
+                            streams[i % 2].cuda_stream)
+        lg, act = m.forward(fwd_ids, fwd_mask, mp, mm, qt)  # synchronizes its own stream
+        torch.cuda.synchronize()
+        for i in range(len(batches)):
+            assert np.array_equal(d_out[i].cpu().numpy(), want[i]), (rep, i)
+        assert np.array_equal(lg, lg_want) and np.array_equal(act, act_want)
+        for t in d_out:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+    m.close()
+
+
+@pytest.mark.parametrize("prec", [FP32, BF16])
+def test_hidden_wider_than_1024_at_batch_one(orc, prec):
+    # D = 1536: the layer norms take the scalar row kernel, so the short
+    # batch's residual GEMMs must not fold split-K partials into them
+    rl, enc, w = synth.make_model(hidden_size=1536, num_hidden_layers=2, num_attention_heads=24,
+                                  intermediate_size=1024, vocab_size=1000, store="BF16",
+                                  max_position_embeddings=512, head_layers=1, seed=71)
+    cfg = synth.flat_cfg(rl, enc)
+    ids, mask, lens = synth.make_batch(1, 120, 120, 120, cfg["vocab_size"], seed=72)
+    mp, mm, qt = synth.make_markers(lens, 4, [(0, 4)], seed=72)
+    om = orc.model(w, cfg)
+    m = sj.Model(w, cfg, precision=prec)
+    assert valid_err(m.encode(ids, mask), om.encode(ids, mask), mask) <= TOL[prec]
+    lg, act = m.forward(ids, mask, mp, mm, qt)
+    ref_lg, ref_act = om.forward(ids, mask, mp, mm, qt)
+    assert probs_err(orc, lg, ref_lg, mm) <= 5e-3
+    assert float(np.abs(act - ref_act).max()) <= 5e-3
     m.close()
 
 
