@@ -139,6 +139,23 @@ int sjh_model_forward(sjh_model* m, const int64_t* ids, const int64_t* mask,
 int sjh_model_encode_device(sjh_model* m, const int32_t* d_ids, const int32_t* h_lens, int32_t B,
                             float* d_hidden, sjh_stream_t stream);
 
+/* sjh_model_encode_device without any device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, same results bit for bit (the same kernels on the same launch
+ * sizes); the work runs launch by launch (no graph) and every intermediate
+ * buffer lives in one fixed array of SJH_NOALLOC_SCRATCH_BYTES per device,
+ * shared by all models on that device and held until the process ends.
+ * Limits: at most 256 sequences, and the batch must fit the array (about
+ * 3000 tokens of a 768-wide bf16 model); larger batches fail with
+ * SJH_E_INVALID and a message naming the bytes needed.  Calls that overlap on
+ * one device (any model, any stream) race on the array: the caller
+ * serializes them.  The call waits for earlier calls of the same model on
+ * any stream and does not synchronize. */
+#define SJH_NOALLOC_SCRATCH_BYTES (32u << 20)
+int sjh_model_encode_device_noalloc(sjh_model* m, const int32_t* d_ids, const int32_t* h_lens,
+                                    int32_t B, float* d_hidden, sjh_stream_t stream);
+
 /* Hidden size, heads, n_act and the precision a model was built with. */
 int sjh_model_info(const sjh_model* m, int32_t* D, int32_t* H, int32_t* n_act,
                    int32_t* precision);

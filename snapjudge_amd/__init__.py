@@ -71,6 +71,8 @@ _SIGS = {
                                     C.c_int32, C.c_int32, _fp, _fp]),
     "sjh_model_encode_device": (C.c_int, [C.c_void_p, C.c_void_p, _i32p, C.c_int32, C.c_void_p,
                                           C.c_void_p]),
+    "sjh_model_encode_device_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, _i32p, C.c_int32,
+                                                  C.c_void_p, C.c_void_p]),
     "sjh_model_info": (C.c_int, [C.c_void_p, _i32p, _i32p, _i32p, _i32p]),
     "sjh_model_graph_stats": (C.c_int, [C.c_void_p, _i32p, _i64p, _i64p]),
     "sjh_model_profile": (C.c_int, [C.c_void_p, C.c_int32]),
@@ -275,6 +277,12 @@ class Model:
         lens = np.ascontiguousarray(lens, dtype=np.int32)
         check(lib().sjh_model_encode_device(self._h, C.c_void_p(d_ids), lens.ctypes.data_as(_i32p),
                                             len(lens), C.c_void_p(d_hidden), C.c_void_p(stream)))
+
+    def encode_device_noalloc(self, d_ids: int, lens: np.ndarray, d_hidden: int, stream: int = 0):
+        lens = np.ascontiguousarray(lens, dtype=np.int32)
+        check(lib().sjh_model_encode_device_noalloc(self._h, C.c_void_p(d_ids),
+                                                    lens.ctypes.data_as(_i32p), len(lens),
+                                                    C.c_void_p(d_hidden), C.c_void_p(stream)))
 
     def graph_stats(self) -> dict:
         n, cap, rep = C.c_int32(), C.c_int64(), C.c_int64()

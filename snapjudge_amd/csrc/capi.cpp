@@ -33,6 +33,9 @@ int guarded(Fn&& fn) {
   } catch (const std::bad_alloc&) {
     g_last_error = "snapjudge HIP: host allocation failed";
     return SJH_E_OOM;
+  } catch (const sjh::ArgError& e) {
+    g_last_error = e.what();
+    return SJH_E_INVALID;
   } catch (const std::runtime_error& e) {
     g_last_error = e.what();
     const std::string s = e.what();
@@ -121,6 +124,15 @@ int sjh_model_encode_device(sjh_model* m, const int32_t* d_ids, const int32_t* h
     if (!m) sjh::fail("null model");
     if (B < 0) sjh::fail("negative batch");
     m->eng->encode_device(d_ids, h_lens, B, d_hidden, as_stream(stream));
+  });
+}
+
+int sjh_model_encode_device_noalloc(sjh_model* m, const int32_t* d_ids, const int32_t* h_lens,
+                                    int32_t B, float* d_hidden, sjh_stream_t stream) {
+  return guarded([&] {
+    if (!m) sjh::fail("null model");
+    if (B < 0) sjh::fail("negative batch");
+    m->eng->encode_device_noalloc(d_ids, h_lens, B, d_hidden, as_stream(stream));
   });
 }
 

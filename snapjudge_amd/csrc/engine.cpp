@@ -170,6 +170,35 @@ const T* off(const void* base, int64_t elems, int dt) {
 
 }  // namespace
 
+// ------------------------------------------------------------------ scratch --
+// The workspace of sjh_model_encode_device_noalloc: one array per device,
+// shared by every model on that device, held until the process ends.  Host
+// code never names it directly (its host-side symbol is a stand-in, not a
+// device address); each device's address comes from hipGetSymbolAddress with
+// that device current, once, and is kept here.
+namespace {
+constexpr size_t kScratchBytes = SJH_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxDevices] = {};
+
+// The calling thread's current device must be `dev`.
+char* scratch_for_device(int dev) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (dev < 0 || dev >= kMaxDevices) fail("device ordinal out of range for the scratch table");
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+}  // namespace
+
 // ------------------------------------------------------------------ engine --
 Engine::Engine(const sjh_model_desc& d, const sjh_options& o) {
   dev_ = o.device;
@@ -215,6 +244,8 @@ Engine::Engine(const sjh_model_desc& d, const sjh_options& o) {
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
   hip_check(hipEventCreateWithFlags(&ev_done_, hipEventDisableTiming), "hipEventCreate");
   hip_check(hipEventCreateWithFlags(&ev_upload_, hipEventDisableTiming), "hipEventCreate");
+  hip_check(hipEventCreateWithFlags(&ev_null_, hipEventDisableTiming), "hipEventCreate");
+  scratch_ = scratch_for_device(dev_);
   stage_weights(d);
 }
 
@@ -529,7 +560,7 @@ void Engine::end_call(hipStream_t st) {
 
 // ------------------------------------------------------------------ launches --
 void Engine::prof_begin(hipStream_t st) {
-  if (!profile_) return;
+  if (!profile_ || quiet_) return;
   hipEvent_t e;
   if (!ev_pool_.empty()) {
     e = ev_pool_.back();
@@ -542,7 +573,7 @@ void Engine::prof_begin(hipStream_t st) {
 }
 
 void Engine::prof_end(const char* name, hipStream_t st) {
-  if (!profile_) return;
+  if (!profile_ || quiet_) return;
   hipEvent_t e;
   if (!ev_pool_.empty()) {
     e = ev_pool_.back();
@@ -1098,12 +1129,86 @@ void Engine::encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, f
   ensure_workspace(p.Tb, p.Bb);
   begin_call(st);
   if (!stream) {
-    if (!ev_null_) hip_check(hipEventCreateWithFlags(&ev_null_, hipEventDisableTiming), "event");
     hip_check(hipEventRecord(ev_null_, nullptr), "record null stream");
     hip_check(hipStreamWaitEvent(st, ev_null_, 0), "wait null stream");
   }
   set_seq_table(p, h_lens, ws_.seq, st);
   run_device_maybe_graph(p, d_ids, d_hidden, false, st);
+  end_call(st);
+  if (!stream) {
+    hip_check(hipEventRecord(ev_null_, st), "record model stream");
+    hip_check(hipStreamWaitEvent(nullptr, ev_null_, 0), "null stream waits");
+  }
+}
+
+size_t Engine::scratch_layout(const BatchPlan& p, Ws& ws) const {
+  // the regions of ensure_workspace, for the plan's bucket, 256-byte aligned;
+  // split-K partials (residual GEMMs of at most 256 rows: up to 16 slices of
+  // [Tb, D]) only where the bucket takes that path
+  const size_t t = static_cast<size_t>(p.Tb), D = D_, as = dt_size(act_dt_);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  const size_t seq = take(seq_table_ints(p.Bb) * 4);
+  const size_t tok_pos = take(t * 4), tok_seq = take(t * 4);
+  const size_t Y = take(t * D * as), QKV = take(t * 3 * D * as), O = take(t * D * as);
+  const size_t G = take(t * static_cast<size_t>(F_) * as);
+  const size_t Z = lora_r_ > 0 ? take(t * static_cast<size_t>(lora_r_) * 4) : 0;
+  const size_t part_floats = p.Tb <= 256 ? 16 * t * D : 0;
+  const size_t part = take(part_floats * 4);
+  ws = Ws();
+  if (off > kScratchBytes) return off;
+  ws.seq = reinterpret_cast<int32_t*>(scratch_ + seq);
+  ws.tok_pos = reinterpret_cast<int*>(scratch_ + tok_pos);
+  ws.tok_seq = reinterpret_cast<int*>(scratch_ + tok_seq);
+  ws.Y = scratch_ + Y;
+  ws.QKV = scratch_ + QKV;
+  ws.O = scratch_ + O;
+  ws.G = scratch_ + G;
+  ws.Z = lora_r_ > 0 ? reinterpret_cast<float*>(scratch_ + Z) : nullptr;
+  ws.partial = part_floats ? reinterpret_cast<float*>(scratch_ + part) : nullptr;
+  ws.partial_cap = static_cast<int64_t>(part_floats);
+  return off;
+}
+
+void Engine::encode_device_noalloc(const int32_t* d_ids, const int32_t* h_lens, int B,
+                                   float* d_hidden, hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(mu_);
+  hip_check(hipSetDevice(dev_), "hipSetDevice");
+  if (B <= 0) return;
+  require(d_ids && h_lens && d_hidden, "encode_device_noalloc: null argument");
+  if (B > kSeqTableMaxB)
+    fail_arg("encode_device_noalloc: at most " + std::to_string(kSeqTableMaxB) + " sequences per call");
+  BatchPlan p = plan_lens(h_lens, B);
+  if (p.T == 0) return;
+  Ws w;
+  const size_t need = scratch_layout(p, w);
+  if (!w.seq) {
+    const size_t D = D_, as = dt_size(act_dt_);
+    const size_t per_tok = 8 + (5 * D + static_cast<size_t>(F_)) * as + static_cast<size_t>(lora_r_) * 4;
+    fail_arg("encode_device_noalloc: this batch (" + std::to_string(p.T) + " tokens, launched as " +
+         std::to_string(p.Tb) + ") needs " + std::to_string(need) +
+         " bytes of scratch; the fixed scratch array holds " + std::to_string(kScratchBytes) +
+         " bytes, about " + std::to_string(kScratchBytes / per_tok) + " tokens of this model");
+  }
+  hipStream_t st = stream ? stream : stream_;
+  begin_call(st);
+  if (!stream) {
+    hip_check(hipEventRecord(ev_null_, nullptr), "record null stream");
+    hip_check(hipStreamWaitEvent(st, ev_null_, 0), "wait null stream");
+  }
+  quiet_ = true;
+  try {
+    launch_seq_table(h_lens, p.B, p.Bb, w.seq, st);
+    run_device(p, w, d_ids, d_hidden, false, st);
+  } catch (...) {
+    quiet_ = false;
+    throw;
+  }
+  quiet_ = false;
   end_call(st);
   if (!stream) {
     hip_check(hipEventRecord(ev_null_, st), "record model stream");

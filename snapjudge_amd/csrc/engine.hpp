@@ -114,6 +114,11 @@ class Engine {
                float* logits, float* act);
   void encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, float* d_hidden,
                      hipStream_t stream);
+  // encode_device with every buffer carved out of the library's fixed
+  // per-device scratch array: no device allocation, no graph, no pinned
+  // staging.  Throws when the batch does not fit the array.
+  void encode_device_noalloc(const int32_t* d_ids, const int32_t* h_lens, int B,
+                             float* d_hidden, hipStream_t stream);
 
   void set_profile(bool on);
   void graph_stats(int32_t* cached, int64_t* captures, int64_t* replays);
@@ -171,7 +176,13 @@ class Engine {
   void prof_end(const char* name, hipStream_t st);
   void prof_collect();
 
+  // Buffers of one forward carved out of the scratch array for plan p, or
+  // the number of bytes that would take when it does not fit (ws.seq null).
+  size_t scratch_layout(const BatchPlan& p, Ws& ws) const;
+
   int dev_ = 0;
+  char* scratch_ = nullptr;  // this device's copy of the scratch array (engine.cpp)
+  bool quiet_ = false;       // no per-launch profile events (the no-allocation path)
   int prec_ = SJH_PREC_BF16;
   int act_dt_ = DT_BF16;  // activation / GEMM operand type
   bool w8_ = false;       // encoder projections stored as fp8 e4m3 + per-row scales

@@ -12,6 +12,14 @@ namespace sjh {
   throw std::runtime_error("snapjudge HIP: " + what);
 }
 
+// A caller's argument the call cannot serve (the C ABI returns SJH_E_INVALID).
+struct ArgError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+[[noreturn]] inline void fail_arg(const std::string& what) {
+  throw ArgError("snapjudge HIP: " + what);
+}
+
 inline void require(bool ok, const char* what) {
   if (!ok) fail(what);
 }
