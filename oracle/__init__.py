@@ -4,8 +4,10 @@ TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, never by the product (snapjudge_amd).
 
   Oracle     -- liboracle.so, the C restatement of the reference path
+               (DecisionModel; SjModel through Oracle.sj_model)
   RefModel   -- oracle/_ref/libsjref.so, the reference's own CPU forward
                 (DecisionModel::load/encode/forward) compiled from its sources
+  RefSjModel -- the same library's SjModel::load/encode/forward
 """
 from __future__ import annotations
 
@@ -177,6 +179,9 @@ class Oracle:
     def model(self, weights: dict, cfg: dict) -> "OracleModel":
         return OracleModel(self, weights, cfg)
 
+    def sj_model(self, weights: dict, cfg: dict) -> "OracleSjModel":
+        return OracleSjModel(self, weights, cfg)
+
 
 class OracleModel:
     def __init__(self, orc: Oracle, weights: dict, cfg: dict):
@@ -338,4 +343,142 @@ class RefModel:
         if self.lib().sjref_forward(self.h, a(ids), a(mask), a(mp), a(mm), a(qt), B, L, K,
                                     a(logits), a(act)) != 0:
             raise RuntimeError(self.lib().sjref_last_error().decode())
+        return logits, act
+
+
+# ---------------------------------------------------------------- SjModel
+class OrcSjLayer(C.Structure):
+    _fields_ = [(n, _fp) for n in ("an_w", "an_b", "q_w", "q_b", "k_w", "k_b", "v_w", "v_b",
+                                   "o_w", "o_b", "fn_w", "fn_b", "w1_w", "w1_b", "w2_w", "w2_b")]
+
+
+class OrcSjModel(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in ("D", "H", "F", "V", "n_layers", "max_pos", "head_layers",
+                                         "head_ff")] + [
+        ("eps", C.c_float), ("word_emb", _fp), ("pos_emb", _fp), ("emb_norm_w", _fp),
+        ("emb_norm_b", _fp), ("layers", C.POINTER(OrcSjLayer)), ("final_norm_w", _fp),
+        ("final_norm_b", _fp), ("type_emb", _fp), ("head", C.POINTER(OrcSjLayer)),
+        ("sc_n_w", _fp), ("sc_n_b", _fp), ("sc_w1", _fp), ("sc_b1", _fp), ("sc_w2", _fp),
+        ("sc_b2", _fp)]
+
+
+def _sj_layer(w, p, n1, n2):
+    g = lambda s: _p(w[p + s])
+    return OrcSjLayer(g(n1 + ".weight"), g(n1 + ".bias"),
+                      g("attn.q.weight"), g("attn.q.bias"), g("attn.k.weight"), g("attn.k.bias"),
+                      g("attn.v.weight"), g("attn.v.bias"), g("attn.o.weight"), g("attn.o.bias"),
+                      g(n2 + ".weight"), g(n2 + ".bias"), g("ffn.w1.weight"), g("ffn.w1.bias"),
+                      g("ffn.w2.weight"), g("ffn.w2.bias"))
+
+
+class OracleSjModel:
+    """The C restatement of SjModel (orc_sj_encode / orc_sj_forward) on a
+    tensor dict with the sj.* names and an sj_config dict."""
+
+    def __init__(self, orc: "Oracle", weights: dict, cfg: dict):
+        L = orc.L
+        v = C.c_void_p
+        L.orc_sj_encode.argtypes = [v, v, v, C.c_int64, C.c_int64, v]
+        L.orc_sj_encode.restype = C.c_int
+        L.orc_sj_forward.argtypes = [v, v, v, v, v, v, C.c_int64, C.c_int64, C.c_int64, v, v, v]
+        L.orc_sj_forward.restype = C.c_int
+        self.orc = orc
+        w = {k: np.ascontiguousarray(x, np.float32) for k, x in weights.items()}
+        D, nl, nh = cfg["hidden_size"], cfg["num_layers"], cfg.get("head_layers", 1)
+        layers = (OrcSjLayer * nl)(*[_sj_layer(w, f"sj.encoder.layers.{i}.", "attn_norm", "ffn_norm")
+                                     for i in range(nl)])
+        head = (OrcSjLayer * max(nh, 1))(*[_sj_layer(w, f"sj.head.layers.{i}.", "norm1", "norm2")
+                                           for i in range(nh)])
+        m = OrcSjModel()
+        m.D, m.H, m.F, m.V = D, cfg["num_heads"], cfg.get("intermediate_size", 4 * D), cfg["vocab_size"]
+        m.n_layers, m.max_pos = nl, cfg.get("max_positions", 512)
+        m.head_layers, m.head_ff = nh, cfg.get("head_intermediate", 4 * D)
+        m.eps = cfg.get("norm_eps", 1e-5)
+        m.word_emb, m.pos_emb = _p(w["sj.embeddings.word.weight"]), _p(w["sj.embeddings.position.weight"])
+        m.emb_norm_w, m.emb_norm_b = _p(w["sj.embeddings.norm.weight"]), _p(w["sj.embeddings.norm.bias"])
+        m.layers, m.head = layers, head
+        m.final_norm_w = _p(w["sj.encoder.final_norm.weight"])
+        m.final_norm_b = _p(w["sj.encoder.final_norm.bias"])
+        m.type_emb = _p(w["sj.type_emb.weight"])
+        m.sc_n_w, m.sc_n_b = _p(w["sj.scorer.norm.weight"]), _p(w["sj.scorer.norm.bias"])
+        m.sc_w1, m.sc_b1 = _p(w["sj.scorer.w1.weight"]), _p(w["sj.scorer.w1.bias"])
+        m.sc_w2, m.sc_b2 = _p(w["sj.scorer.w2.weight"]), _p(w["sj.scorer.w2.bias"])
+        self._keep = (w, layers, head)
+        self.m, self.D = m, D
+
+    def encode(self, ids, mask):
+        ids = np.ascontiguousarray(ids, np.int64)
+        mask = np.ascontiguousarray(mask, np.int64)
+        B, L = ids.shape
+        out = np.empty((B, L, self.D), np.float32)
+        a = Oracle._a
+        assert self.orc.L.orc_sj_encode(C.byref(self.m), a(ids), a(mask), B, L, a(out)) == 0
+        return out
+
+    def forward(self, ids, mask, marker_pos, marker_mask, qtype, hidden=False):
+        ids = np.ascontiguousarray(ids, np.int64)
+        mask = np.ascontiguousarray(mask, np.int64)
+        mp = np.ascontiguousarray(marker_pos, np.int64)
+        mm = np.ascontiguousarray(marker_mask, np.uint8)
+        qt = np.ascontiguousarray(qtype, np.int64)
+        B, L = ids.shape
+        K = mp.shape[1]
+        logits = np.empty((B, K), np.float32)
+        act = np.empty((B, 2), np.float32)
+        h = np.empty((B, L, self.D), np.float32) if hidden else None
+        a = Oracle._a
+        assert self.orc.L.orc_sj_forward(C.byref(self.m), a(ids), a(mask), a(mp), a(mm), a(qt), B, L,
+                                         K, a(logits), a(act), a(h) if h is not None else None) == 0
+        return (logits, act, h) if hidden else (logits, act)
+
+
+class RefSjModel:
+    """The reference's own SjModel (oracle/_ref/libsjref.so) on a checkpoint
+    dir with sj_config.json + model.safetensors."""
+
+    def __init__(self, ckpt_dir: str):
+        L = RefModel.lib()
+        v = C.c_void_p
+        L.sjref_sj_load.argtypes = [C.c_char_p]
+        L.sjref_sj_load.restype = v
+        L.sjref_sj_free.argtypes = [v]
+        L.sjref_sj_encode.argtypes = [v, v, v, C.c_int64, C.c_int64, v]
+        L.sjref_sj_forward.argtypes = [v, v, v, v, v, v, C.c_int64, C.c_int64, C.c_int64, v, v]
+        self.L = L
+        self.h = L.sjref_sj_load(ckpt_dir.encode())
+        if not self.h:
+            raise RuntimeError(L.sjref_last_error().decode())
+        import json
+        with open(os.path.join(ckpt_dir, "sj_config.json")) as f:
+            self.D = json.load(f)["hidden_size"]
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.sjref_sj_free(self.h)
+            self.h = None
+
+    def encode(self, ids, mask):
+        ids = np.ascontiguousarray(ids, np.int64)
+        mask = np.ascontiguousarray(mask, np.int64)
+        B, L = ids.shape
+        out = np.empty((B, L, self.D), np.float32)
+        a = Oracle._a
+        if self.L.sjref_sj_encode(self.h, a(ids), a(mask), B, L, a(out)) != 0:
+            raise RuntimeError(self.L.sjref_last_error().decode())
+        return out
+
+    def forward(self, ids, mask, marker_pos, marker_mask, qtype):
+        ids = np.ascontiguousarray(ids, np.int64)
+        mask = np.ascontiguousarray(mask, np.int64)
+        mp = np.ascontiguousarray(marker_pos, np.int64)
+        mm = np.ascontiguousarray(marker_mask, np.uint8)
+        qt = np.ascontiguousarray(qtype, np.int64)
+        B, L = ids.shape
+        K = mp.shape[1]
+        logits = np.empty((B, K), np.float32)
+        act = np.empty((B, 2), np.float32)
+        a = Oracle._a
+        if self.L.sjref_sj_forward(self.h, a(ids), a(mask), a(mp), a(mm), a(qt), B, L, K,
+                                   a(logits), a(act)) != 0:
+            raise RuntimeError(self.L.sjref_last_error().decode())
         return logits, act

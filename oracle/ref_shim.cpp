@@ -17,10 +17,12 @@
 #include "nlohmann/json.hpp"
 #include "snapjudge/model.hpp"
 #include "snapjudge/safetensors.hpp"
+#include "snapjudge/sj_model.hpp"
 #include "snapjudge/tensor.hpp"
 
 using nlohmann::json;
 using snapjudge::DecisionModel;
+using snapjudge::SjModel;
 using snapjudge::Tensor;
 
 namespace {
@@ -117,6 +119,63 @@ int sjref_forward(void* mp, const int64_t* ids, const int64_t* mask, const int64
     for (int64_t b = 0; b < B; ++b) {
       std::memcpy(logits + b * K, lg[static_cast<size_t>(b)].data(), sizeof(float) * static_cast<size_t>(K));
       std::memcpy(act + b * A, ac[static_cast<size_t>(b)].data(), sizeof(float) * static_cast<size_t>(A));
+    }
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+// ---- SjModel (src/sj_model.cpp) ----
+// Loads <dir>/sj_config.json and <dir>/model.safetensors, the layout
+// SjTrainModel and SjPretrain read (src/sj_train.cpp:180-184).
+void* sjref_sj_load(const char* dir) {
+  try {
+    std::string d(dir);
+    json cfg;
+    std::ifstream(d + "/sj_config.json") >> cfg;
+    auto w = snapjudge::SafeTensors::load(d + "/model.safetensors");
+    return SjModel::load(cfg, w, d).release();
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return nullptr;
+  }
+}
+
+void sjref_sj_free(void* m) { delete static_cast<SjModel*>(m); }
+
+int sjref_sj_encode(void* mp, const int64_t* ids, const int64_t* mask, int64_t B, int64_t L,
+                    float* out) {
+  try {
+    auto* m = static_cast<SjModel*>(mp);
+    auto h = m->encode(rows_i64(ids, B, L), rows_i64(mask, B, L));
+    const int64_t D = m->D();
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t i = 0; i < L; ++i)
+        std::memcpy(out + (b * L + i) * D, h[static_cast<size_t>(b)][static_cast<size_t>(i)].data(),
+                    sizeof(float) * static_cast<size_t>(D));
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+int sjref_sj_forward(void* mp, const int64_t* ids, const int64_t* mask, const int64_t* marker_pos,
+                     const uint8_t* marker_mask, const int64_t* qtype, int64_t B, int64_t L,
+                     int64_t K, float* logits, float* act) {
+  try {
+    auto* m = static_cast<SjModel*>(mp);
+    std::vector<std::vector<uint8_t>> mm(static_cast<size_t>(B));
+    for (int64_t b = 0; b < B; ++b) mm[static_cast<size_t>(b)].assign(marker_mask + b * K, marker_mask + (b + 1) * K);
+    std::vector<int64_t> qt(qtype, qtype + B);
+    std::vector<std::vector<float>> lg, ac;
+    m->forward(rows_i64(ids, B, L), rows_i64(mask, B, L), rows_i64(marker_pos, B, K), mm, qt,
+               lg, ac);
+    for (int64_t b = 0; b < B; ++b) {
+      std::memcpy(logits + b * K, lg[static_cast<size_t>(b)].data(), sizeof(float) * static_cast<size_t>(K));
+      std::memcpy(act + b * 2, ac[static_cast<size_t>(b)].data(), sizeof(float) * 2);
     }
     return 0;
   } catch (const std::exception& e) {

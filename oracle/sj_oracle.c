@@ -451,3 +451,153 @@ double orc_confidence_from_probs(const double* p, int k) {
 
 /* src/common.cpp:232-237 -- round half to even at 1e-4. */
 double orc_round4(double v) { return nearbyint(v * 1e4) / 1e4; }
+
+/* ------------------------------------------------------------------ SjModel */
+
+/* src/sj_model.cpp:44-85 -- self_attention: q, k, v = three separate
+ * projections with biases ([M, D] each), split into [B, H, L, Dh], full
+ * attention over the first lens[b] keys (no window, no RoPE), merged back and
+ * projected by o (+ bias).  Writes the projected output [M, D]. */
+static void sj_self_attention(const float* Y, int64_t B, int64_t H, int64_t L, int64_t Dh,
+                              const int64_t* lens, const orc_sj_layer* ly, float* out) {
+  const int64_t D = H * Dh, M = B * L;
+  float* q = ORC_ALLOC(M * D, float);
+  float* k = ORC_ALLOC(M * D, float);
+  float* v = ORC_ALLOC(M * D, float);
+  float* qkv = ORC_ALLOC(M * 3 * D, float);
+  float* Q = ORC_ALLOC(M * D, float);
+  float* Kt = ORC_ALLOC(M * D, float);
+  float* V = ORC_ALLOC(M * D, float);
+  float* At = ORC_ALLOC(M * D, float);
+  float* AO = ORC_ALLOC(M * D, float);
+  orc_gemm_nt(Y, ly->q_w, ly->q_b, 0, M, D, D, q);
+  orc_gemm_nt(Y, ly->k_w, ly->k_b, 0, M, D, D, k);
+  orc_gemm_nt(Y, ly->v_w, ly->v_b, 0, M, D, D, v);
+  /* packed (q|k|v) rows, then the same [B, H, L, Dh] split as the
+   * DecisionModel path (pure copies: the permute of src/sj_model.cpp:57-71) */
+  for (int64_t r = 0; r < M; ++r) {
+    memcpy(qkv + r * 3 * D, q + r * D, sizeof(float) * (size_t)D);
+    memcpy(qkv + r * 3 * D + D, k + r * D, sizeof(float) * (size_t)D);
+    memcpy(qkv + r * 3 * D + 2 * D, v + r * D, sizeof(float) * (size_t)D);
+  }
+  split_heads(qkv, B, L, H, Dh, Q, Kt, V);
+  orc_attention(Q, Kt, V, lens, B, H, L, Dh, 0, At);
+  merge_heads(At, B, L, H, Dh, AO);
+  orc_gemm_nt(AO, ly->o_w, ly->o_b, 0, M, D, D, out);
+  free(q); free(k); free(v); free(qkv); free(Q); free(Kt); free(V); free(At); free(AO);
+}
+
+/* One pre-norm layer (src/sj_model.cpp:240-252 for the encoder, :308-318 for
+ * the head): X += attn(LN(X)); X += W2 . gelu(W1 . LN(X) + b1) + b2. */
+static void sj_layer(float* X, int64_t B, int64_t H, int64_t L, int64_t Dh, int64_t F,
+                     const int64_t* lens, const orc_sj_layer* ly, float eps) {
+  const int64_t D = H * Dh, M = B * L;
+  float* Y = ORC_ALLOC(M * D, float);
+  float* P = ORC_ALLOC(M * D, float);
+  float* G = ORC_ALLOC(M * F, float);
+  orc_layer_norm(X, M, D, ly->an_w, ly->an_b, eps, Y);
+  sj_self_attention(Y, B, H, L, Dh, lens, ly, P);
+  add_inplace(X, P, M * D);
+  orc_layer_norm(X, M, D, ly->fn_w, ly->fn_b, eps, Y);
+  orc_gemm_nt(Y, ly->w1_w, ly->w1_b, 1, M, F, D, G);
+  orc_gemm_nt(G, ly->w2_w, ly->w2_b, 0, M, D, F, P);
+  add_inplace(X, P, M * D);
+  free(Y); free(P); free(G);
+}
+
+/* src/sj_model.cpp:206-255 -- run_encoder: word embedding + learned position
+ * embedding of row r at position r % L clamped to max_pos - 1, summed in
+ * float, LayerNorm with bias; the layers; the final LayerNorm with bias. */
+static void sj_run_encoder(const orc_sj_model* m, const int64_t* ids, const int64_t* lens,
+                           int64_t B, int64_t L, float* h) {
+  const int64_t D = m->D, H = m->H, Dh = D / H, M = B * L;
+  float* X = ORC_ALLOC(M * D, float);
+  float* E = ORC_ALLOC(M * D, float);
+  orc_embedding(m->word_emb, D, ids, M, E);
+  for (int64_t r = 0; r < M; ++r) {
+    int64_t pos = r % L;
+    if (pos >= m->max_pos) pos = m->max_pos - 1;
+    add_inplace(E + r * D, m->pos_emb + pos * D, D);
+  }
+  orc_layer_norm(E, M, D, m->emb_norm_w, m->emb_norm_b, m->eps, X);
+  for (int64_t li = 0; li < m->n_layers; ++li)
+    sj_layer(X, B, H, L, Dh, m->F, lens, &m->layers[li], m->eps);
+  orc_layer_norm(X, M, D, m->final_norm_w, m->final_norm_b, m->eps, h);
+  free(X); free(E);
+}
+
+int orc_sj_encode(const orc_sj_model* m, const int64_t* ids, const int64_t* mask, int64_t B,
+                  int64_t L, float* out) {
+  if (B <= 0) return 0;
+  int64_t* lens = ORC_ALLOC(B, int64_t);
+  lens_from_mask(mask, B, L, lens);
+  sj_run_encoder(m, ids, lens, B, L, out);
+  free(lens);
+  return 0;
+}
+
+/* src/sj_model.cpp:277-368 */
+int orc_sj_forward(const orc_sj_model* m, const int64_t* ids, const int64_t* mask,
+                   const int64_t* marker_pos, const uint8_t* marker_mask, const int64_t* qtype,
+                   int64_t B, int64_t L, int64_t K, float* logits, float* act, float* hidden_out) {
+  if (B <= 0) return 0;
+  const int64_t D = m->D, H = m->H, Dh = D / H, M = B * L;
+  int64_t* lens = ORC_ALLOC(B, int64_t);
+  lens_from_mask(mask, B, L, lens);
+  float* h = ORC_ALLOC(M * D, float);
+  sj_run_encoder(m, ids, lens, B, L, h);
+  /* :291-298 h += type_emb[qtype] on every position */
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t i = 0; i < L; ++i)
+      add_inplace(h + (b * L + i) * D, m->type_emb + qtype[b] * D, D);
+  /* :300-321 head layers: the encoder's layer shape, GELU FFN of width
+   * head_intermediate, LayerNorm eps = norm_eps */
+  for (int64_t li = 0; li < m->head_layers; ++li)
+    sj_layer(h, B, H, L, Dh, m->head_ff, lens, &m->head[li], m->eps);
+  if (hidden_out) memcpy(hidden_out, h, sizeof(float) * (size_t)(M * D));
+  /* :323-347 scorer on the marker rows (positions clamped to [0, L-1]) */
+  {
+    float* mk = ORC_ALLOC(B * K * D, float);
+    float* s0 = ORC_ALLOC(B * K * D, float);
+    float* s1 = ORC_ALLOC(B * K * D, float);
+    float* s2 = ORC_ALLOC(B * K, float);
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t kk = 0; kk < K; ++kk) {
+        int64_t p = marker_pos[b * K + kk];
+        if (p < 0) p = 0;
+        if (p >= L) p = L - 1;
+        memcpy(mk + (b * K + kk) * D, h + (b * L + p) * D, sizeof(float) * (size_t)D);
+      }
+    orc_layer_norm(mk, B * K, D, m->sc_n_w, m->sc_n_b, m->eps, s0);
+    orc_gemm_nt(s0, m->sc_w1, m->sc_b1, 1, B * K, D, D, s1);
+    orc_gemm_nt(s1, m->sc_w2, m->sc_b2, 0, B * K, 1, D, s2);
+    for (int64_t i = 0; i < B * K; ++i) logits[i] = marker_mask[i] ? s2[i] : -1e4f;
+    free(mk); free(s0); free(s1); free(s2);
+  }
+  /* :349-367 act = {top1, 1 - top1} of softmax(logits): float exp of the
+   * max-subtracted logit, double sum and division */
+  {
+    double* p = ORC_ALLOC(K, double);
+    for (int64_t b = 0; b < B; ++b) {
+      const float* lg = logits + b * K;
+      float mx = lg[0];
+      for (int64_t j = 1; j < K; ++j) mx = lg[j] > mx ? lg[j] : mx;
+      double s = 0.0;
+      for (int64_t j = 0; j < K; ++j) {
+        p[j] = (double)expf(lg[j] - mx);
+        s += p[j];
+      }
+      double top1 = 0.0;
+      for (int64_t j = 0; j < K; ++j) {
+        p[j] /= s;
+        top1 = j == 0 || p[j] > top1 ? p[j] : top1;
+      }
+      act[b * 2 + 0] = (float)top1;
+      act[b * 2 + 1] = (float)(1.0 - top1);
+    }
+    free(p);
+  }
+  free(h);
+  free(lens);
+  return 0;
+}

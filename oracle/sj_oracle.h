@@ -102,6 +102,42 @@ int orc_forward(const orc_model* m, const int64_t* ids, const int64_t* mask,
                 const int64_t* qtype, int64_t B, int64_t L, int64_t K, float* logits,
                 float* act, float* hidden_out);
 
+/* ---- SjModel, snapjudge's own BERT-style model (src/sj_model.cpp) ---- */
+
+/* One layer of the encoder or of the head (src/sj_model.cpp EncLayer /
+ * HeadLayer, include/snapjudge/sj_model.hpp:79-101): pre-norm attention with
+ * separate q/k/v/o projections and biases, then a pre-norm GELU FFN with
+ * biases.  For a head layer n1 -> an_*, n2 -> fn_*. */
+typedef struct {
+  const float *an_w, *an_b;             /* [D] */
+  const float *q_w, *q_b, *k_w, *k_b;   /* [D, D], [D] */
+  const float *v_w, *v_b, *o_w, *o_b;   /* [D, D], [D] */
+  const float *fn_w, *fn_b;             /* [D] */
+  const float *w1_w, *w1_b;             /* [F, D], [F] */
+  const float *w2_w, *w2_b;             /* [D, F], [D] */
+} orc_sj_layer;
+
+typedef struct {
+  int64_t D, H, F, V, n_layers, max_pos, head_layers, head_ff;
+  float eps;
+  const float *word_emb, *pos_emb;      /* [V, D], [max_pos, D] */
+  const float *emb_norm_w, *emb_norm_b; /* [D] */
+  const orc_sj_layer* layers;           /* F = intermediate_size */
+  const float *final_norm_w, *final_norm_b;
+  const float* type_emb;                /* [n_types, D] */
+  const orc_sj_layer* head;             /* F = head_intermediate */
+  const float *sc_n_w, *sc_n_b, *sc_w1, *sc_b1, *sc_w2, *sc_b2;
+} orc_sj_model;
+
+/* SjModel::encode (src/sj_model.cpp:257-275): [B, L, D], padding included. */
+int orc_sj_encode(const orc_sj_model* m, const int64_t* ids, const int64_t* mask, int64_t B,
+                  int64_t L, float* out);
+/* SjModel::forward (src/sj_model.cpp:277-368): logits [B, K] (masked -1e4),
+ * act [B, 2] = {top1, 1 - top1}; optionally the post-head hidden [B, L, D]. */
+int orc_sj_forward(const orc_sj_model* m, const int64_t* ids, const int64_t* mask,
+                   const int64_t* marker_pos, const uint8_t* marker_mask, const int64_t* qtype,
+                   int64_t B, int64_t L, int64_t K, float* logits, float* act, float* hidden_out);
+
 /* ---- answer decoding (src/agent.cpp:256-266, src/common.cpp:199-237) ---- */
 double orc_clamp_temperature(double t);
 void orc_calibrated_probs(const float* logits, int k, double t_scale, double* p);

@@ -89,3 +89,45 @@ def test_ops_bit_exact(orc):
         out = np.empty_like(q)
         L.sjref_attention(p(q), p(k), p(v), p(lens), 2, 3, 11, 8, win, p(out))
         assert np.array_equal(out, orc.attention(q, k, v, lens, win))
+
+
+def test_sj_model_bit_exact(orc, tmp_path):
+    # SjModel (src/sj_model.cpp): learned positions (rows past max_positions
+    # clamp to the last one), biased LayerNorms, separate q/k/v/o with biases,
+    # GELU FFNs, a head of two layers and the scorer; padded rows included
+    from oracle import RefSjModel
+
+    cfg, w = synth.make_sj_model(hidden_size=48, num_layers=2, num_heads=3, vocab_size=200,
+                                 intermediate_size=80, max_positions=20, head_layers=2,
+                                 head_intermediate=64, seed=13)
+    synth.write_sj_checkpoint(str(tmp_path), cfg, w, store="F32")
+    ref = RefSjModel(str(tmp_path))
+    om = orc.sj_model(w, cfg)
+    ids, mask, lens = synth.make_batch(4, 26, 3, 26, cfg["vocab_size"], seed=14)
+    mp, mm, qt = synth.make_markers(lens, 4, [(0, 4), (1, 3), (2, 2), (0, 1)], seed=14)
+    mp[1, 0] = 40  # clamped to L - 1
+    assert np.array_equal(om.encode(ids, mask), ref.encode(ids, mask))
+    lo_, ao = om.forward(ids, mask, mp, mm, qt)
+    lr, ar = ref.forward(ids, mask, mp, mm, qt)
+    assert np.array_equal(lo_, lr) and np.array_equal(ao, ar)
+    assert np.all(lo_[mm == 0] == np.float32(-1e4))
+    # act is {top1, 1 - top1} of the softmax over the (masked) logits
+    for b in range(len(lo_)):
+        p = np.exp(lo_[b].astype(np.float64) - lo_[b].max())
+        assert abs(ao[b, 0] - (p / p.sum()).max()) < 1e-6
+        assert abs(ao[b, 0] + ao[b, 1] - 1.0) < 1e-6
+
+
+def test_sj_model_catches_a_dropped_bias(orc, tmp_path):
+    # the oracle run without one layer's attention output bias no longer
+    # matches the reference: the comparison above is sensitive to it
+    from oracle import RefSjModel
+
+    cfg, w = synth.make_sj_model(hidden_size=32, num_layers=1, num_heads=2, vocab_size=100,
+                                 max_positions=16, seed=15)
+    synth.write_sj_checkpoint(str(tmp_path), cfg, w, store="F32")
+    ref = RefSjModel(str(tmp_path))
+    w2 = dict(w)
+    w2["sj.encoder.layers.0.attn.o.bias"] = np.zeros_like(w["sj.encoder.layers.0.attn.o.bias"])
+    ids, mask, _ = synth.make_batch(2, 10, 4, 10, cfg["vocab_size"], seed=16)
+    assert not np.allclose(orc.sj_model(w2, cfg).encode(ids, mask), ref.encode(ids, mask), atol=1e-4)
