@@ -199,6 +199,38 @@ def test_cfg3_shape_sampled_rows_and_batch_invariance(orc):
     m.close()
 
 
+@pytest.fixture(scope="module")
+def cfg4(golden_dir):
+    g = np.load(os.path.join(golden_dir, "cfg4_b4s8192.npz"))
+    rl, enc, w = synth.make_model(**synth.PRESETS["cfg4"], seed=int(g["seed"]))
+    cfg = synth.flat_cfg(rl, enc)
+    ids, mask, lens = synth.make_batch(4, 8192, 4096, 8192, cfg["vocab_size"], seed=int(g["batch_seed"]))
+    assert np.array_equal(lens, g["lens"])  # the bench's batch
+    return cfg, w, g, ids, mask, lens
+
+
+@pytest.mark.parametrize("prec", [BF16, FP32])
+def test_cfg4_full_depth_vs_reference_fixture(cfg4, prec):
+    # BASELINE config 4 at full depth: 22 layers, batch 4 x seq 8192, lengths
+    # U[4096, 8192] (T ~ 27k tokens on the persistent GEMMs, RoPE positions up
+    # to 8191, attention over up to 8k keys).  The fixture holds the compiled
+    # reference's encode of the shortest and the longest row, each run alone
+    # (rows are independent), at sampled positions (first and last 16, every
+    # 97th in between)
+    cfg, w, g, ids, mask, lens = cfg4
+    print(f"cfg4 22 layers prec={prec} T={int(lens.sum())}", flush=True)
+    m = sj.Model(w, cfg, precision=prec)
+    h = m.encode(ids, mask)
+    m.close()
+    for name, b in (("short", int(g["rows"][0])), ("long", int(g["rows"][1]))):
+        pos = g["pos_" + name]
+        err = float(np.abs(h[b, pos] - g["hidden_" + name]).max())
+        print(f"cfg4 prec={prec} row {b} (n={int(lens[b])}, {len(pos)} positions) max|d|={err:.3g}",
+              flush=True)
+        assert err <= TOL[prec]
+    assert np.all(h[~mask.astype(bool)] == 0)
+
+
 def test_graph_replay_serves_a_shape_bucket():
     # Batches of different sizes, lengths and ids that fall in one shape
     # bucket replay one captured graph; each result equals the same batch run
