@@ -120,6 +120,26 @@ void sjh_default_options(sjh_options* opt);
 int sjh_model_create(const sjh_model_desc* desc, const sjh_options* opt, sjh_model** out);
 void sjh_model_destroy(sjh_model* m);
 
+/* Loads a checkpoint directory straight into device memory, with no fp32
+ * host copy of the model (the reference materialises one:
+ * src/safetensors.cpp:109-135, src/model.cpp:96-171).  model.safetensors is
+ * memory-mapped; each tensor is copied to the device in its stored type and
+ * converted there (bf16 weights of a bf16 model are copied as they are).
+ *   DecisionModel (DecisionModel::load, src/model.cpp:35-205):
+ *     rl_agent_config.json, encoder/config.json, model.safetensors.
+ *     The four encoder projections may also be stored as "F8_E4M3" codes
+ *     with an F32 "<name>_scale" of one scale per output row (the
+ *     SJH_PREC_FP8W format, see sjh_quantize_fp8); such a checkpoint needs
+ *     SJH_PREC_FP8W.  F32/F16/BF16 projections loaded with SJH_PREC_FP8W are
+ *     quantized on the device, bit-identical to sjh_quantize_fp8.
+ *   SjModel (SjModel::load, src/sj_model.cpp:87-204): sj_config.json and
+ *     model.safetensors with the sj.* tensors.  Its act head is
+ *     {top1, 1 - top1} (n_act 2) and positions past max_positions use the
+ *     last row of the position table, as the reference does.
+ * Same configuration keys, defaults, strict shapes and error cases as the
+ * reference loaders (SJH_E_INVALID with the message). */
+int sjh_model_load(const char* dir, const sjh_options* opt, sjh_model** out);
+
 /* DecisionModel::encode (src/model.cpp:222-307).  ids, mask: [B, L] int64,
  * right-padded, mask 0/1.  hidden: [B, L, D] fp32, caller-allocated. */
 int sjh_model_encode(sjh_model* m, const int64_t* ids, const int64_t* mask, int32_t B, int32_t L,

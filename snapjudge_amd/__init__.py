@@ -66,6 +66,7 @@ _SIGS = {
     "sjh_default_options": (None, [C.POINTER(Options)]),
     "sjh_model_create": (C.c_int, [C.POINTER(ModelDesc), C.POINTER(Options), C.POINTER(C.c_void_p)]),
     "sjh_model_destroy": (None, [C.c_void_p]),
+    "sjh_model_load": (C.c_int, [C.c_char_p, C.POINTER(Options), C.POINTER(C.c_void_p)]),
     "sjh_model_encode": (C.c_int, [C.c_void_p, _i64p, _i64p, C.c_int32, C.c_int32, _fp]),
     "sjh_model_forward": (C.c_int, [C.c_void_p, _i64p, _i64p, _i64p, _u8p, _i64p, C.c_int32,
                                     C.c_int32, C.c_int32, _fp, _fp]),
@@ -236,6 +237,23 @@ class Model:
         self.D = D
         self.n_act = d.n_act
         self.precision = precision
+
+    @classmethod
+    def load(cls, path: str, precision: int = SJH_PREC_BF16, max_len: int = 0,
+             use_graphs: bool = True, pad_rows: bool = False, device: int = 0) -> "Model":
+        """A checkpoint directory loaded straight to the device (sjh_model_load):
+        a DecisionModel (rl_agent_config.json + encoder/config.json) or an
+        SjModel (sj_config.json), with model.safetensors."""
+        self = cls.__new__(cls)
+        opt = Options(precision, max_len, 1 if use_graphs else 0, 1 if pad_rows else 0, device)
+        h = C.c_void_p()
+        check(lib().sjh_model_load(os.fsencode(path), C.byref(opt), C.byref(h)))
+        self._h = h
+        self._keep = None
+        D, n_act = C.c_int32(), C.c_int32()
+        check(lib().sjh_model_info(h, C.byref(D), None, C.byref(n_act), None))
+        self.D, self.n_act, self.precision = D.value, n_act.value, precision
+        return self
 
     def close(self):
         if getattr(self, "_h", None):

@@ -8,10 +8,12 @@
 
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <new>
 #include <stdexcept>
 #include <string>
 
+#include "ckpt.hpp"
 #include "engine.hpp"
 #include "sjh_host.hpp"
 #include "sjh_kernels.hpp"
@@ -84,7 +86,27 @@ int sjh_model_create(const sjh_model_desc* desc, const sjh_options* opt, sjh_mod
     if (opt) o = *opt;
     auto* m = new sjh_model{nullptr};
     try {
-      m->eng = new sjh::Engine(*desc, o);
+      m->eng = new sjh::Engine(sjh::source_from_desc(*desc), o);
+    } catch (...) {
+      delete m;
+      throw;
+    }
+    *out = m;
+  });
+}
+
+int sjh_model_load(const char* dir, const sjh_options* opt, sjh_model** out) {
+  return guarded([&] {
+    if (!dir || !out) sjh::fail_arg("sjh_model_load: null argument");
+    *out = nullptr;
+    sjh_options o;
+    sjh_default_options(&o);
+    if (opt) o = *opt;
+    // the mapping stays open until every tensor is on the device
+    std::unique_ptr<sjh::Checkpoint> ck = sjh::read_checkpoint(dir);
+    auto* m = new sjh_model{nullptr};
+    try {
+      m->eng = new sjh::Engine(ck->src, o);
     } catch (...) {
       delete m;
       throw;

@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstring>
 
+#include "sjh_fp8.hpp"
 #include "sjh_host.hpp"
 
 namespace sjh {
@@ -57,32 +58,16 @@ void PinnedBuf::ensure(size_t bytes) {
   bytes_ = bytes;
 }
 
-// OCP e4m3fn (1 sign, 4 exponent bits with bias 7, 3 mantissa bits; no
-// infinity, S.1111.111 is NaN, largest finite 448), round to nearest with
-// ties to even; magnitudes of 448 and above (and infinities) saturate to 448.
 uint8_t fp8_e4m3_rne(float x) {
   uint32_t u;
   std::memcpy(&u, &x, 4);
-  const uint8_t sign = static_cast<uint8_t>((u >> 24) & 0x80u);
-  const uint32_t a = u & 0x7fffffffu;
-  if (a > 0x7f800000u) return sign | 0x7f;   // NaN
-  if (a >= 0x43e00000u) return sign | 0x7e;  // >= 448
-  if (a < 0x3c800000u) {                     // below 2^-6: subnormal steps of 2^-9
-    float f;
-    std::memcpy(&f, &a, 4);
-    const float m = std::nearbyint(f * 512.0f);  // exact scaling; default mode rounds to even
-    return sign | static_cast<uint8_t>(m);       // m == 8 is the smallest normal, code 0x08
-  }
-  // normal: round the 23-bit mantissa to 3 bits (ties to even); a carry
-  // moves into the exponent
-  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
-  const uint32_t code = ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
-  return sign | static_cast<uint8_t>(code > 0x7eu ? 0x7eu : code);
+  return fp8_e4m3_rne_bits(u);
 }
 
 // Per-row symmetric quantization: scale[r] = max |w[r, :]| / 448 (1 for an
 // all-zero row), q[r, c] = e4m3(w[r, c] / scale[r]).  Row r then stands for
-// decode(q[r, :]) * scale[r].
+// decode(q[r, :]) * scale[r].  convert.hip's device quantizer computes the
+// same codes and scales.
 void quantize_fp8_rows(const float* w, size_t rows, size_t cols, uint8_t* q, float* scale) {
   for (size_t r = 0; r < rows; ++r) {
     const float* row = w + r * cols;
@@ -91,61 +76,13 @@ void quantize_fp8_rows(const float* w, size_t rows, size_t cols, uint8_t* q, flo
       const float v = std::fabs(row[c]);
       if (v > amax) amax = v;  // NaN compares false
     }
-    const float sc = (amax > 0.f && std::isfinite(amax)) ? amax / 448.0f : 1.0f;
+    const float sc = fp8_row_scale(amax);
     scale[r] = sc;
     for (size_t c = 0; c < cols; ++c) q[r * cols + c] = fp8_e4m3_rne(row[c] / sc);
   }
 }
 
 namespace {
-uint16_t bf16_rne(float f) {
-  uint32_t u;
-  std::memcpy(&u, &f, 4);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
-
-DevBuf upload_f32(const float* src, size_t n, const char* what) {
-  if (!src) fail(std::string("model descriptor: missing ") + what);
-  DevBuf b;
-  b.alloc(n * sizeof(float));
-  hip_check(hipMemcpy(b.get(), src, n * sizeof(float), hipMemcpyHostToDevice), what);
-  return b;
-}
-
-DevBuf upload_bf16(const float* src, size_t n, const char* what) {
-  if (!src) fail(std::string("model descriptor: missing ") + what);
-  std::vector<uint16_t> tmp(n);
-  for (size_t i = 0; i < n; ++i) tmp[i] = bf16_rne(src[i]);
-  DevBuf b;
-  b.alloc(n * sizeof(uint16_t));
-  hip_check(hipMemcpy(b.get(), tmp.data(), n * sizeof(uint16_t), hipMemcpyHostToDevice), what);
-  return b;
-}
-
-// Row-wise fp8 weights: rows x cols codes plus one fp32 scale per row.
-struct Fp8Dev {
-  DevBuf q, scale;
-};
-
-Fp8Dev upload_fp8(const float* src, size_t rows, size_t cols, const char* what) {
-  if (!src) fail(std::string("model descriptor: missing ") + what);
-  std::vector<uint8_t> q(rows * cols);
-  std::vector<float> sc(rows);
-  quantize_fp8_rows(src, rows, cols, q.data(), sc.data());
-  Fp8Dev d;
-  d.q.alloc(q.size());
-  d.scale.alloc(rows * sizeof(float));
-  hip_check(hipMemcpy(d.q.get(), q.data(), q.size(), hipMemcpyHostToDevice), what);
-  hip_check(hipMemcpy(d.scale.get(), sc.data(), rows * sizeof(float), hipMemcpyHostToDevice), what);
-  return d;
-}
-
-DevBuf upload_opt_f32(const float* src, size_t n, const char* what) {
-  return src ? upload_f32(src, n, what) : DevBuf();
-}
-
 // RoPE tables exactly as src/model.cpp:173-190: inverse frequency and angle in
 // double, cos/sin rounded to float; [max_pos, Dh/2].
 void rope_table(double theta, int max_pos, int Dh, std::vector<float>& c, std::vector<float>& s) {
@@ -200,7 +137,83 @@ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 }  // namespace
 
 // ------------------------------------------------------------------ engine --
-Engine::Engine(const sjh_model_desc& d, const sjh_options& o) {
+ModelSource source_from_desc(const sjh_model_desc& d) {
+  ModelSource s;
+  s.arch = ARCH_MODERNBERT;
+  s.act_head = ACT_MLP;
+  s.D = d.hidden_size;
+  s.H = d.num_heads;
+  s.F = d.intermediate_size;
+  s.V = d.vocab_size;
+  s.n_layers = d.num_layers;
+  s.max_pos = d.max_position;
+  s.n_act = d.n_act;
+  s.head_layers = d.head_layers;
+  s.lora_r = (d.lora_a && d.lora_b) ? d.lora_r : 0;
+  s.eps = d.norm_eps;
+  s.head_ff = 4 * d.hidden_size;
+  s.head_eps = 1e-5f;
+  s.head_act = 2;
+  s.theta_full = d.rope_theta_full;
+  s.theta_sliding = d.rope_theta_sliding;
+  const int64_t D = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
+  auto h = [](const float* p, int64_t n) { return Src::host_f32(p, n); };
+  auto hm = [](const float* p, int64_t n) {
+    Mat m;
+    m.w = Src::host_f32(p, n);
+    return m;
+  };
+  s.emb_w = h(d.emb_w, V * D);
+  s.emb_norm = h(d.emb_norm, D);
+  s.final_norm = h(d.final_norm, D);
+  s.rope_cos_full = d.rope_cos_full;
+  s.rope_sin_full = d.rope_sin_full;
+  s.rope_cos_slide = d.rope_cos_slide;
+  s.rope_sin_slide = d.rope_sin_slide;
+  if (d.num_layers > 0 && !d.layers) fail("model descriptor: missing layers");
+  for (int i = 0; i < d.num_layers; ++i) {
+    const sjh_layer_desc& l = d.layers[i];
+    LayerSrc ly;
+    ly.attn_norm = h(l.attn_norm, D);
+    ly.wqkv = hm(l.wqkv, 3 * D * D);
+    ly.wo = hm(l.wo, D * D);
+    ly.mlp_norm = h(l.mlp_norm, D);
+    ly.wi = hm(l.wi, 2 * F * D);
+    ly.wo2 = hm(l.wo2, D * F);
+    ly.window = l.window;
+    ly.sliding = l.sliding;
+    s.layers.push_back(ly);
+  }
+  if (s.lora_r > 0) {
+    s.lora_a = h(d.lora_a, s.lora_r * D);
+    s.lora_b = h(d.lora_b, D * s.lora_r);
+  }
+  s.type_emb = h(d.type_emb, 3 * D);
+  if (d.head_layers > 0 && !d.head) fail("model descriptor: missing head layers");
+  for (int i = 0; i < d.head_layers; ++i) {
+    const sjh_head_desc& hd = d.head[i];
+    HeadSrc x;
+    x.n1w = h(hd.n1w, D), x.n1b = h(hd.n1b, D), x.n2w = h(hd.n2w, D), x.n2b = h(hd.n2b, D);
+    x.in_w = h(hd.in_w, 3 * D * D), x.in_b = h(hd.in_b, 3 * D);
+    x.out_w = h(hd.out_w, D * D), x.out_b = h(hd.out_b, D);
+    x.l1w = h(hd.l1w, 4 * D * D), x.l1b = h(hd.l1b, 4 * D);
+    x.l2w = h(hd.l2w, D * 4 * D), x.l2b = h(hd.l2b, D);
+    s.head.push_back(x);
+  }
+  s.sc_ln_w = h(d.sc_ln_w, D);
+  s.sc_ln_b = h(d.sc_ln_b, D);
+  s.sc_w1 = h(d.sc_w1, D * D);
+  s.sc_b1 = h(d.sc_b1, D);
+  s.sc_w2 = h(d.sc_w2, D);
+  s.sc_b2 = h(d.sc_b2, 1);
+  s.act_w1 = h(d.act_w1, 256 * (D + 4));
+  s.act_b1 = h(d.act_b1, 256);
+  s.act_w2 = h(d.act_w2, static_cast<int64_t>(d.n_act) * 256);
+  s.act_b2 = h(d.act_b2, d.n_act);
+  return s;
+}
+
+Engine::Engine(const ModelSource& src, const sjh_options& o) {
   dev_ = o.device;
   int ndev = 0;
   hip_check(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
@@ -220,33 +233,58 @@ Engine::Engine(const sjh_model_desc& d, const sjh_options& o) {
   use_graphs_ = o.use_graphs != 0;
   pad_rows_ = o.pad_rows != 0;
 
-  D_ = d.hidden_size;
-  H_ = d.num_heads;
-  F_ = d.intermediate_size;
-  V_ = d.vocab_size;
-  nlayers_ = d.num_layers;
-  max_pos_ = d.max_position;
-  n_act_ = d.n_act;
-  head_layers_ = d.head_layers;
-  lora_r_ = (d.lora_a && d.lora_b) ? d.lora_r : 0;
-  eps_ = d.norm_eps;
+  arch_ = src.arch;
+  act_head_ = src.act_head;
+  D_ = src.D;
+  H_ = src.H;
+  F_ = src.F;
+  V_ = src.V;
+  nlayers_ = src.n_layers;
+  max_pos_ = src.max_pos;
+  n_act_ = src.n_act;
+  head_layers_ = src.head_layers;
+  head_ff_ = src.head_ff;
+  head_eps_ = src.head_eps;
+  head_act_ = src.head_act;
+  lora_r_ = src.lora_r;
+  eps_ = src.eps;
+  require(arch_ == ARCH_MODERNBERT || arch_ == ARCH_BERT, "unknown model family");
   require(D_ > 0 && H_ > 0 && D_ % H_ == 0, "hidden_size must be a positive multiple of num_heads");
   Dh_ = D_ / H_;
   require(Dh_ % 2 == 0, "head_dim must be even");
   require(F_ > 0 && V_ > 0 && nlayers_ > 0 && max_pos_ > 0, "bad model dimensions");
   require(!w8_ || (D_ % 64 == 0 && F_ % 64 == 0),
           "fp8 weights need hidden_size and intermediate_size multiples of 64");
-  require(n_act_ > 0 && head_layers_ >= 0 && lora_r_ >= 0, "bad head dimensions");
-  require(d.layers != nullptr, "model descriptor: missing layers");
-  require(head_layers_ == 0 || d.head != nullptr, "model descriptor: missing head layers");
-  max_len_ = o.max_len > 0 ? std::min(o.max_len, max_pos_) : max_pos_;
+  require(n_act_ > 0 && head_layers_ >= 0 && lora_r_ >= 0 && (head_layers_ == 0 || head_ff_ > 0),
+          "bad head dimensions");
+  require(act_head_ != ACT_TOP1 || n_act_ == 2, "the top-1 act head has two outputs");
+  require(static_cast<int>(src.layers.size()) == nlayers_ &&
+              static_cast<int>(src.head.size()) == head_layers_,
+          "model source: layer count mismatch");
+  // ModernBERT rows are bounded by the RoPE tables; the BERT family clamps
+  // positions past its table to the last row (src/sj_model.cpp:229-236), so
+  // its rows are bounded only by the caller's max_len
+  if (arch_ == ARCH_BERT)
+    max_len_ = o.max_len > 0 ? o.max_len : (1 << 24);
+  else
+    max_len_ = o.max_len > 0 ? std::min(o.max_len, max_pos_) : max_pos_;
 
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
   hip_check(hipEventCreateWithFlags(&ev_done_, hipEventDisableTiming), "hipEventCreate");
   hip_check(hipEventCreateWithFlags(&ev_upload_, hipEventDisableTiming), "hipEventCreate");
   hip_check(hipEventCreateWithFlags(&ev_null_, hipEventDisableTiming), "hipEventCreate");
-  scratch_ = scratch_for_device(dev_);
-  stage_weights(d);
+  try {
+    scratch_ = scratch_for_device(dev_);
+    stage_weights(src);
+    hip_check(hipStreamSynchronize(stream_), "weight staging");
+  } catch (...) {  // the destructor does not run for a constructor that throws
+    (void)hipStreamSynchronize(stream_);
+    (void)hipEventDestroy(ev_null_);
+    (void)hipEventDestroy(ev_done_);
+    (void)hipEventDestroy(ev_upload_);
+    (void)hipStreamDestroy(stream_);
+    throw;
+  }
 }
 
 Engine::~Engine() {
@@ -266,93 +304,199 @@ Engine::~Engine() {
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
-void Engine::stage_weights(const sjh_model_desc& d) {
-  const size_t D = D_, F = F_;
-  auto upload_w = [&](const float* p, size_t n, const char* what) {
-    return act_dt_ == DT_BF16 ? upload_bf16(p, n, what) : upload_f32(p, n, what);
-  };
-  emb_w_ = upload_w(d.emb_w, static_cast<size_t>(V_) * D, "emb_w");
-  emb_norm_ = upload_f32(d.emb_norm, D, "emb_norm");
-  final_norm_ = upload_f32(d.final_norm, D, "final_norm");
-
-  const size_t nt = static_cast<size_t>(max_pos_) * (Dh_ / 2);
-  std::vector<float> c, s;
-  if (d.rope_cos_full && d.rope_sin_full) {
-    rope_cos_full_ = upload_f32(d.rope_cos_full, nt, "rope_cos_full");
-    rope_sin_full_ = upload_f32(d.rope_sin_full, nt, "rope_sin_full");
-  } else {
-    rope_table(d.rope_theta_full, max_pos_, Dh_, c, s);
-    rope_cos_full_ = upload_f32(c.data(), nt, "rope_cos_full");
-    rope_sin_full_ = upload_f32(s.data(), nt, "rope_sin_full");
+// ---- staging: every segment of a source goes to consecutive elements of one
+// device buffer.  fp32 and bf16 segments that already have the target type
+// are copied as they are; others are converted on the device (convert.hip)
+// from a temporary copy of their bytes, which is released once the
+// conversion has run.
+DevBuf Engine::put_f32(const Src& s, int64_t n, const char* what) {
+  if (s.empty()) fail(std::string("model: missing ") + what);
+  if (s.numel() != n) fail(std::string("model: wrong size of ") + what);
+  DevBuf d;
+  d.alloc(static_cast<size_t>(n) * 4);
+  int64_t off = 0;
+  for (const Seg& g : s.segs) {
+    float* dst = d.as<float>() + off;
+    if (g.type == SRC_F32) {
+      hip_check(hipMemcpy(dst, g.p, static_cast<size_t>(g.n) * 4, hipMemcpyHostToDevice), what);
+    } else if (g.type == SRC_BF16 || g.type == SRC_F16) {
+      DevBuf tmp;
+      tmp.alloc(static_cast<size_t>(g.n) * 2);
+      hip_check(hipMemcpy(tmp.get(), g.p, static_cast<size_t>(g.n) * 2, hipMemcpyHostToDevice), what);
+      launch_widen_f32(tmp.get(), g.type, dst, g.n, stream_);
+      hip_check(hipStreamSynchronize(stream_), what);
+    } else {
+      fail(std::string("model: ") + what + " cannot be stored as e4m3 codes");
+    }
+    off += g.n;
   }
-  if (d.rope_cos_slide && d.rope_sin_slide) {
-    rope_cos_slide_ = upload_f32(d.rope_cos_slide, nt, "rope_cos_slide");
-    rope_sin_slide_ = upload_f32(d.rope_sin_slide, nt, "rope_sin_slide");
+  return d;
+}
+
+DevBuf Engine::put_f32_opt(const Src& s, int64_t n, const char* what) {
+  return s.empty() ? DevBuf() : put_f32(s, n, what);
+}
+
+DevBuf Engine::put_act(const Src& s, int64_t n, const char* what) {
+  if (act_dt_ == DT_F32) return put_f32(s, n, what);
+  if (s.empty()) fail(std::string("model: missing ") + what);
+  if (s.numel() != n) fail(std::string("model: wrong size of ") + what);
+  DevBuf d;
+  d.alloc(static_cast<size_t>(n) * 2);
+  int64_t off = 0;
+  for (const Seg& g : s.segs) {
+    uint16_t* dst = d.as<uint16_t>() + off;
+    if (g.type == SRC_BF16) {
+      hip_check(hipMemcpy(dst, g.p, static_cast<size_t>(g.n) * 2, hipMemcpyHostToDevice), what);
+    } else if (g.type == SRC_F32 || g.type == SRC_F16) {
+      const size_t es = g.type == SRC_F32 ? 4 : 2;
+      DevBuf tmp;
+      tmp.alloc(static_cast<size_t>(g.n) * es);
+      hip_check(hipMemcpy(tmp.get(), g.p, static_cast<size_t>(g.n) * es, hipMemcpyHostToDevice), what);
+      launch_narrow_bf16(tmp.get(), g.type, dst, g.n, stream_);
+      hip_check(hipStreamSynchronize(stream_), what);
+    } else {
+      fail(std::string("model: ") + what + " holds e4m3 codes; load it with SJH_PREC_FP8W");
+    }
+    off += g.n;
+  }
+  return d;
+}
+
+Engine::Fp8Dev Engine::put_fp8(const Mat& m, int64_t rows, int64_t cols, const char* what) {
+  if (m.w.empty()) fail(std::string("model: missing ") + what);
+  if (m.w.numel() != rows * cols) fail(std::string("model: wrong size of ") + what);
+  Fp8Dev d;
+  d.q.alloc(static_cast<size_t>(rows * cols));
+  d.scale.alloc(static_cast<size_t>(rows) * 4);
+  bool codes = true, values = true;
+  for (const Seg& g : m.w.segs) (g.type == SRC_F8 ? values : codes) = false;
+  if (codes) {  // stored e4m3 rows and their scales: copied as they are
+    if (m.scale.numel() != rows) fail(std::string("model: ") + what + " needs one scale per row");
+    int64_t off = 0;
+    for (const Seg& g : m.w.segs) {
+      hip_check(hipMemcpy(d.q.as<uint8_t>() + off, g.p, static_cast<size_t>(g.n), hipMemcpyHostToDevice), what);
+      off += g.n;
+    }
+    off = 0;
+    for (const Seg& g : m.scale.segs) {
+      if (g.type != SRC_F32) fail(std::string("model: scales of ") + what + " must be fp32");
+      hip_check(hipMemcpy(d.scale.as<float>() + off, g.p, static_cast<size_t>(g.n) * 4, hipMemcpyHostToDevice), what);
+      off += g.n;
+    }
+  } else if (values) {  // quantized here, with the host quantizer's arithmetic
+    DevBuf w = put_f32(m.w, rows * cols, what);
+    launch_quantize_fp8_rows(w.as<float>(), rows, cols, d.q.as<uint8_t>(), d.scale.as<float>(), stream_);
+    hip_check(hipStreamSynchronize(stream_), what);
   } else {
-    rope_table(d.rope_theta_sliding, max_pos_, Dh_, c, s);
-    rope_cos_slide_ = upload_f32(c.data(), nt, "rope_cos_slide");
-    rope_sin_slide_ = upload_f32(s.data(), nt, "rope_sin_slide");
+    fail(std::string("model: ") + what + " mixes e4m3 codes and other types");
+  }
+  return d;
+}
+
+void Engine::stage_weights(const ModelSource& s) {
+  const int64_t D = D_, F = F_;
+  const bool bert = arch_ == ARCH_BERT;
+  emb_w_ = put_act(s.emb_w, static_cast<int64_t>(V_) * D, "emb_w");
+  emb_norm_ = put_f32(s.emb_norm, D, "emb_norm");
+  final_norm_ = put_f32(s.final_norm, D, "final_norm");
+  if (bert) {
+    pos_emb_ = put_f32(s.pos_emb, static_cast<int64_t>(max_pos_) * D, "position embedding");
+    emb_norm_b_ = put_f32(s.emb_norm_b, D, "emb_norm bias");
+    final_norm_b_ = put_f32(s.final_norm_b, D, "final_norm bias");
+  } else {
+    const int64_t nt = static_cast<int64_t>(max_pos_) * (Dh_ / 2);
+    std::vector<float> c, sn;
+    auto table = [&](const float* hc, const float* hs, double theta, DevBuf& dc, DevBuf& ds,
+                     const char* what) {
+      if (hc && hs) {
+        dc = put_f32(Src::host_f32(hc, nt), nt, what);
+        ds = put_f32(Src::host_f32(hs, nt), nt, what);
+      } else {
+        rope_table(theta, max_pos_, Dh_, c, sn);
+        dc = put_f32(Src::host_f32(c.data(), nt), nt, what);
+        ds = put_f32(Src::host_f32(sn.data(), nt), nt, what);
+      }
+    };
+    table(s.rope_cos_full, s.rope_sin_full, s.theta_full, rope_cos_full_, rope_sin_full_,
+          "rope tables (full)");
+    table(s.rope_cos_slide, s.rope_sin_slide, s.theta_sliding, rope_cos_slide_, rope_sin_slide_,
+          "rope tables (sliding)");
   }
 
+  // ModernBERT: Wi [2F, D] feeds GEGLU; BERT: w1 [F, D] feeds GELU
+  const int64_t wi_rows = bert ? F : 2 * F;
   layers_.resize(static_cast<size_t>(nlayers_));
   for (int i = 0; i < nlayers_; ++i) {
-    const sjh_layer_desc& s0 = d.layers[i];
+    const LayerSrc& s0 = s.layers[static_cast<size_t>(i)];
     LayerDev& L = layers_[static_cast<size_t>(i)];
-    L.has_attn_norm = s0.attn_norm != nullptr;
-    if (L.has_attn_norm) L.attn_norm = upload_f32(s0.attn_norm, D, "attn_norm");
-    L.mlp_norm = upload_f32(s0.mlp_norm, D, "mlp_norm");
+    L.has_attn_norm = !s0.attn_norm.empty();
+    require(!bert || L.has_attn_norm, "model: every BERT layer has an attention norm");
+    if (L.has_attn_norm) L.attn_norm = put_f32(s0.attn_norm, D, "attn_norm");
+    L.attn_norm_b = put_f32_opt(s0.attn_norm_b, D, "attn_norm bias");
+    L.mlp_norm = put_f32(s0.mlp_norm, D, "mlp_norm");
+    L.mlp_norm_b = put_f32_opt(s0.mlp_norm_b, D, "mlp_norm bias");
     if (w8_) {  // the four projections as per-row fp8 (src/model.cpp:96-128 shapes)
-      Fp8Dev a = upload_fp8(s0.wqkv, 3 * D, D, "wqkv"), b = upload_fp8(s0.wo, D, D, "wo"),
-             c2 = upload_fp8(s0.wi, 2 * F, D, "wi"), e = upload_fp8(s0.wo2, D, F, "wo2");
+      Fp8Dev a = put_fp8(s0.wqkv, 3 * D, D, "wqkv"), b = put_fp8(s0.wo, D, D, "wo"),
+             c2 = put_fp8(s0.wi, wi_rows, D, "wi"), e = put_fp8(s0.wo2, D, F, "wo2");
       L.wqkv = std::move(a.q), L.wqkv_s = std::move(a.scale);
       L.wo = std::move(b.q), L.wo_s = std::move(b.scale);
       L.wi = std::move(c2.q), L.wi_s = std::move(c2.scale);
       L.wo2 = std::move(e.q), L.wo2_s = std::move(e.scale);
     } else {
-      L.wqkv = upload_w(s0.wqkv, 3 * D * D, "wqkv");
-      L.wo = upload_w(s0.wo, D * D, "wo");
-      L.wi = upload_w(s0.wi, 2 * F * D, "wi");
-      L.wo2 = upload_w(s0.wo2, D * F, "wo2");
+      L.wqkv = put_act(s0.wqkv.w, 3 * D * D, "wqkv");
+      L.wo = put_act(s0.wo.w, D * D, "wo");
+      L.wi = put_act(s0.wi.w, wi_rows * D, "wi");
+      L.wo2 = put_act(s0.wo2.w, D * F, "wo2");
     }
+    L.wqkv_b = put_f32_opt(s0.wqkv_b, 3 * D, "wqkv bias");
+    L.wo_b = put_f32_opt(s0.wo_b, D, "wo bias");
+    L.wi_b = put_f32_opt(s0.wi_b, wi_rows, "wi bias");
+    L.wo2_b = put_f32_opt(s0.wo2_b, D, "wo2 bias");
     require(s0.window >= 0, "negative attention window");
+    require(!bert || (s0.window == 0 && L.attn_norm_b.get() && L.wqkv_b.get() && L.wo_b.get() &&
+                      L.mlp_norm_b.get() && L.wi_b.get() && L.wo2_b.get()),
+            "model: a BERT-family layer has full attention and a bias on every norm and projection");
     L.window = s0.window;
     L.sliding = s0.sliding;
   }
 
   if (lora_r_ > 0) {
-    lora_a_ = upload_f32(d.lora_a, static_cast<size_t>(lora_r_) * D, "lora_a");
-    lora_b_ = upload_f32(d.lora_b, D * static_cast<size_t>(lora_r_), "lora_b");
+    lora_a_ = put_f32(s.lora_a, static_cast<int64_t>(lora_r_) * D, "lora_a");
+    lora_b_ = put_f32(s.lora_b, D * lora_r_, "lora_b");
   }
-  type_emb_ = upload_f32(d.type_emb, 3 * D, "type_emb");
+  type_emb_ = put_f32(s.type_emb, 3 * D, "type_emb");
+  const int64_t HF = head_ff_;
   head_.resize(static_cast<size_t>(head_layers_));
   for (int i = 0; i < head_layers_; ++i) {
-    const sjh_head_desc& h = d.head[i];
+    const HeadSrc& h = s.head[static_cast<size_t>(i)];
     HeadDev& hd = head_[static_cast<size_t>(i)];
-    hd.n1w = upload_f32(h.n1w, D, "head n1w");
-    hd.n1b = upload_f32(h.n1b, D, "head n1b");
-    hd.n2w = upload_f32(h.n2w, D, "head n2w");
-    hd.n2b = upload_f32(h.n2b, D, "head n2b");
-    hd.in_w = upload_w(h.in_w, 3 * D * D, "head in_w");
-    hd.in_b = upload_f32(h.in_b, 3 * D, "head in_b");
-    hd.out_w = upload_w(h.out_w, D * D, "head out_w");
-    hd.out_b = upload_f32(h.out_b, D, "head out_b");
-    hd.l1w = upload_w(h.l1w, 4 * D * D, "head l1w");
-    hd.l1b = upload_f32(h.l1b, 4 * D, "head l1b");
-    hd.l2w = upload_w(h.l2w, D * 4 * D, "head l2w");
-    hd.l2b = upload_f32(h.l2b, D, "head l2b");
+    hd.n1w = put_f32(h.n1w, D, "head n1w");
+    hd.n1b = put_f32(h.n1b, D, "head n1b");
+    hd.n2w = put_f32(h.n2w, D, "head n2w");
+    hd.n2b = put_f32(h.n2b, D, "head n2b");
+    hd.in_w = put_act(h.in_w, 3 * D * D, "head in_w");
+    hd.in_b = put_f32(h.in_b, 3 * D, "head in_b");
+    hd.out_w = put_act(h.out_w, D * D, "head out_w");
+    hd.out_b = put_f32(h.out_b, D, "head out_b");
+    hd.l1w = put_act(h.l1w, HF * D, "head l1w");
+    hd.l1b = put_f32(h.l1b, HF, "head l1b");
+    hd.l2w = put_act(h.l2w, D * HF, "head l2w");
+    hd.l2b = put_f32(h.l2b, D, "head l2b");
   }
-  sc_ln_w_ = upload_f32(d.sc_ln_w, D, "scorer ln weight");
-  sc_ln_b_ = upload_opt_f32(d.sc_ln_b, D, "scorer ln bias");
-  sc_w1_ = upload_f32(d.sc_w1, D * D, "scorer w1");
-  sc_b1_ = upload_opt_f32(d.sc_b1, D, "scorer b1");
-  sc_w2_ = upload_f32(d.sc_w2, D, "scorer w2");
-  sc_b2_ = upload_opt_f32(d.sc_b2, 1, "scorer b2");
-  act_w1_ = upload_f32(d.act_w1, 256 * (D + 4), "act w1");
-  act_b1_ = upload_f32(d.act_b1, 256, "act b1");
-  act_w2_ = upload_f32(d.act_w2, static_cast<size_t>(n_act_) * 256, "act w2");
-  act_b2_ = upload_f32(d.act_b2, static_cast<size_t>(n_act_), "act b2");
+  sc_ln_w_ = put_f32(s.sc_ln_w, D, "scorer ln weight");
+  sc_ln_b_ = put_f32_opt(s.sc_ln_b, D, "scorer ln bias");
+  sc_w1_ = put_f32(s.sc_w1, D * D, "scorer w1");
+  sc_b1_ = put_f32_opt(s.sc_b1, D, "scorer b1");
+  sc_w2_ = put_f32(s.sc_w2, D, "scorer w2");
+  sc_b2_ = put_f32_opt(s.sc_b2, 1, "scorer b2");
+  if (act_head_ == ACT_MLP) {
+    act_w1_ = put_f32(s.act_w1, 256 * (D + 4), "act w1");
+    act_b1_ = put_f32(s.act_b1, 256, "act b1");
+    act_w2_ = put_f32(s.act_w2, static_cast<int64_t>(n_act_) * 256, "act w2");
+    act_b2_ = put_f32(s.act_b2, n_act_, "act b2");
+  }
 }
-
 
 // ------------------------------------------------------------------ batches --
 namespace {
@@ -494,11 +638,11 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   Y_.ensure(t * D * as);
   QKV_.ensure(t * 3 * D * as);
   O_.ensure(t * D * as);
-  G_.ensure(t * std::max<size_t>(F_, head_layers_ > 0 ? 4 * D : 0) * as);
+  const size_t hff = head_layers_ > 0 ? static_cast<size_t>(head_ff_) : 0;
+  G_.ensure(t * std::max<size_t>(F_, hff) * as);
   if (lora_r_ > 0) Z_.ensure(t * static_cast<size_t>(lora_r_) * 4);
   {  // up to 16 K splits of a 256-row batch over the widest weight matrix
-    const size_t nw = std::max<size_t>({3 * D, 2 * static_cast<size_t>(F_),
-                                        head_layers_ > 0 ? 4 * D : 0});
+    const size_t nw = std::max<size_t>({3 * D, 2 * static_cast<size_t>(F_), hff});
     splitk_.ensure(16 * std::min<size_t>(t, 256) * nw * 4);
   }
   cap_T_ = nT;
@@ -689,7 +833,9 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
 
   launch_token_index(seq_start, q_len, Bb, w.tok_pos, w.tok_seq, st);
 
-  // src/model.cpp:332-340: X = LN(emb[ids]); layer 0 reads X itself
+  // src/model.cpp:332-340: X = LN(emb[ids]); layer 0 reads X itself.  BERT
+  // family (src/sj_model.cpp:220-237): X = LN(word[ids] + pos[position] ; w, b)
+  const bool bert = arch_ == ARCH_BERT;
   {
     LnArgs e;
     e.in = emb_w_.get();
@@ -697,6 +843,13 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
     e.ld_in = D;
     e.ids = d_ids;
     e.w = emb_norm_.as<float>();
+    e.b = emb_norm_b_.as<float>();
+    if (bert) {
+      e.add = pos_emb_.as<float>();
+      e.add_ids = w.tok_pos;
+      e.add_rows = max_pos_;
+      e.ld_add = D;
+    }
     e.eps = eps_;
     e.x_out = X;
     e.ld_x = D;
@@ -722,6 +875,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
     a.ld_in = D;
     a.normalize = ly.has_attn_norm;
     a.w = ly.has_attn_norm ? ly.attn_norm.as<float>() : nullptr;
+    a.b = ly.attn_norm_b.as<float>();
     a.eps = eps_;
     a.y_out = Y;
     a.y_dtype = adt;
@@ -737,6 +891,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
   final_args.in_dtype = DT_F32;
   final_args.ld_in = D;
   final_args.w = final_norm_.as<float>();
+  final_args.b = final_norm_b_.as<float>();
   final_args.eps = eps_;
   final_args.x_out = X;
   final_args.ld_x = D;
@@ -748,7 +903,8 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
     // layers after the first get their attn_norm from the previous layer's
     // Wo2 step (resid_gemm_ln)
     if (li == 0 && ly.has_attn_norm) ln("attn_norm", attn_norm_args(0), st);
-    {  // qkv = Y . Wqkv^T with RoPE on q, k (src/model.cpp:355-365)
+    {  // qkv = Y . Wqkv^T with RoPE on q, k (src/model.cpp:355-365); BERT:
+       // q|k|v rows with their biases, no RoPE (src/sj_model.cpp:44-52)
       GemmArgs g;
       g.A = Y;
       g.lda = D;
@@ -760,17 +916,23 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       g.N = 3 * D;
       g.K = D;
       g.in_dtype = adt;
-      g.epi = EPI_ROPE;
       g.out = QKV;
       g.ldo = 3 * D;
       g.out_dtype = adt;
-      g.pos = w.tok_pos;
-      g.rope_cos = (ly.sliding ? rope_cos_slide_ : rope_cos_full_).as<float>();
-      g.rope_sin = (ly.sliding ? rope_sin_slide_ : rope_sin_full_).as<float>();
-      g.rope_rows = max_pos_;
-      g.rope_dim = D;
-      g.head_dim = Dh_;
-      gemm("gemm_qkv_rope", g, w, st);
+      if (bert) {
+        g.epi = EPI_STORE;
+        g.bias = ly.wqkv_b.as<float>();
+        gemm("gemm_qkv_bias", g, w, st);
+      } else {
+        g.epi = EPI_ROPE;
+        g.pos = w.tok_pos;
+        g.rope_cos = (ly.sliding ? rope_cos_slide_ : rope_cos_full_).as<float>();
+        g.rope_sin = (ly.sliding ? rope_sin_slide_ : rope_sin_full_).as<float>();
+        g.rope_rows = max_pos_;
+        g.rope_dim = D;
+        g.head_dim = Dh_;
+        gemm("gemm_qkv_rope", g, w, st);
+      }
     }
     {  // attention (src/model.cpp:381)
       AttnArgs a;
@@ -809,12 +971,14 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       g.epi = EPI_RESID;
       g.X = X;
       g.ldx = D;
+      g.bias = ly.wo_b.as<float>();
       // Y = mlp_norm(X) (src/model.cpp:392)
       LnArgs a;
       a.in = X;
       a.in_dtype = DT_F32;
       a.ld_in = D;
       a.w = ly.mlp_norm.as<float>();
+      a.b = ly.mlp_norm_b.as<float>();
       a.eps = eps_;
       a.y_out = Y;
       a.y_dtype = adt;
@@ -824,7 +988,8 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       a.D = D;
       resid_gemm_ln("gemm_wo_resid", g, "mlp_norm", a, w, st);
     }
-    {  // G = geglu(Y . Wi^T) (src/model.cpp:394)
+    {  // G = geglu(Y . Wi^T) (src/model.cpp:394); BERT: G = gelu(Y . W1^T + b1)
+       // (src/sj_model.cpp:249)
       GemmArgs g;
       g.A = Y;
       g.lda = D;
@@ -836,11 +1001,18 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       g.N = F;
       g.K = D;
       g.in_dtype = adt;
-      g.epi = EPI_GEGLU;
       g.out = G;
       g.ldo = F;
       g.out_dtype = adt;
-      gemm("gemm_wi_geglu", g, w, st);
+      if (bert) {
+        g.epi = EPI_STORE;
+        g.bias = ly.wi_b.as<float>();
+        g.act = 1;
+        gemm("gemm_w1_gelu", g, w, st);
+      } else {
+        g.epi = EPI_GEGLU;
+        gemm("gemm_wi_geglu", g, w, st);
+      }
     }
     {  // X += G . Wo2^T (src/model.cpp:395-397)
       GemmArgs g;
@@ -857,6 +1029,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       g.epi = EPI_RESID;
       g.X = X;
       g.ldx = D;
+      g.bias = ly.wo2_b.as<float>();
       // then the next layer's attn_norm, or the final norm
       if (li + 1 < nlayers_)
         resid_gemm_ln("gemm_wo2_resid", g, "attn_norm", attn_norm_args(li + 1), w, st);
@@ -897,7 +1070,9 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
   }
 }
 
-// src/model.cpp:409-459: type embedding, then N pre-norm TransformerEncoderLayers.
+// src/model.cpp:409-459: type embedding, then N pre-norm TransformerEncoderLayers
+// (ReLU FFN of width 4D, norms eps 1e-5).  BERT family, src/sj_model.cpp:291-321:
+// the same layer with a GELU FFN of width head_intermediate and eps norm_eps.
 void Engine::enqueue_head_layers(const BatchPlan& p, const Ws& w, float* X, hipStream_t st) {
   const int T = p.Tb, D = D_, Bb = p.Bb;
   const int32_t* si = w.seq;
@@ -914,7 +1089,7 @@ void Engine::enqueue_head_layers(const BatchPlan& p, const Ws& w, float* X, hipS
     a.ld_in = D;
     a.w = hd.n1w.as<float>();
     a.b = hd.n1b.as<float>();
-    a.eps = 1e-5f;
+    a.eps = head_eps_;
     a.y_out = w.Y;
     a.y_dtype = adt;
     a.ld_y = D;
@@ -989,26 +1164,26 @@ void Engine::enqueue_head_layers(const BatchPlan& p, const Ws& w, float* X, hipS
     g1.ldw = D;
     g1.M = T;
     g1.M_dev = T_dev;
-    g1.N = 4 * D;
+    g1.N = head_ff_;
     g1.K = D;
     g1.in_dtype = adt;
     g1.epi = EPI_STORE;
     g1.out = w.G;
-    g1.ldo = 4 * D;
+    g1.ldo = head_ff_;
     g1.out_dtype = adt;
     g1.bias = hd.l1b.as<float>();
-    g1.act = 2;
+    g1.act = head_act_;
     gemm("head_linear1", g1, w, st);
 
     GemmArgs g2;
     g2.A = w.G;
-    g2.lda = 4 * D;
+    g2.lda = head_ff_;
     g2.W = hd.l2w.get();
-    g2.ldw = 4 * D;
+    g2.ldw = head_ff_;
     g2.M = T;
     g2.M_dev = T_dev;
     g2.N = D;
-    g2.K = 4 * D;
+    g2.K = head_ff_;
     g2.in_dtype = adt;
     g2.epi = EPI_RESID;
     g2.X = X;
@@ -1314,6 +1489,10 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     g2.act = 0;
     gemm("scorer_linear2", g2, ws_, st);
   }
+  if (act_head_ == ACT_TOP1) {
+    launch_act_top1(tail_s2_.as<float>(), tail_idx_.as<int32_t>() + nrow, B, K, tail_lg_.as<float>(),
+                    tail_act_.as<float>(), st);
+  } else {
   launch_act_features(tail_s2_.as<float>(), tail_idx_.as<int32_t>() + nrow, B, K,
                       tail_rows_.as<float>() + static_cast<size_t>(nmk) * D, D, D,
                       tail_lg_.as<float>(), tail_ain_.as<float>(), D + 4, st);
@@ -1348,6 +1527,7 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     gemm("act_linear2", g2, ws_, st);
   }
   launch_act_softmax(tail_ao_.as<float>(), B, n_act_, tail_act_.as<float>(), st);
+  }
   hip_check(hipMemcpyAsync(logits, tail_lg_.get(), static_cast<size_t>(nmk) * 4, hipMemcpyDeviceToHost, st),
             "download logits");
   hip_check(hipMemcpyAsync(act, tail_act_.get(), static_cast<size_t>(B) * n_act_ * 4,

@@ -27,8 +27,9 @@
 #include <tuple>
 #include <vector>
 
-#include "snapjudge_hip.h"
+#include "model_src.hpp"
 #include "sjh_kernels.hpp"
+#include "snapjudge_hip.h"
 
 namespace sjh {
 
@@ -100,7 +101,9 @@ struct Ws {
 
 class Engine {
  public:
-  Engine(const sjh_model_desc& d, const sjh_options& o);
+  // Stages every weight of `src` on the device (its host memory may be
+  // released after the constructor returns).
+  Engine(const ModelSource& src, const sjh_options& o);
   ~Engine();
 
   int D() const { return D_; }
@@ -126,10 +129,14 @@ class Engine {
 
  private:
   struct LayerDev {
-    DevBuf attn_norm, wqkv, wo, mlp_norm, wi, wo2;
+    DevBuf attn_norm, attn_norm_b, wqkv, wqkv_b, wo, wo_b, mlp_norm, mlp_norm_b, wi, wi_b, wo2,
+        wo2_b;                         // the biases and norm biases of the BERT family
     DevBuf wqkv_s, wo_s, wi_s, wo2_s;  // per-row scales of fp8 projections
     bool has_attn_norm = false;
     int window = 0, sliding = 0;
+  };
+  struct Fp8Dev {
+    DevBuf q, scale;
   };
   struct HeadDev {
     DevBuf n1w, n1b, n2w, n2b, in_w, in_b, out_w, out_b, l1w, l1b, l2w, l2b;
@@ -140,7 +147,14 @@ class Engine {
   };
   static constexpr size_t kMaxGraphs = 32;
 
-  void stage_weights(const sjh_model_desc& d);
+  void stage_weights(const ModelSource& s);
+  // one tensor of a source to the device: fp32, the activation type, or
+  // per-row e4m3 codes + scales (converted on the device when the source
+  // holds another type)
+  DevBuf put_f32(const Src& s, int64_t n, const char* what);
+  DevBuf put_f32_opt(const Src& s, int64_t n, const char* what);
+  DevBuf put_act(const Src& s, int64_t n, const char* what);
+  Fp8Dev put_fp8(const Mat& m, int64_t rows, int64_t cols, const char* what);
   BatchPlan plan(const int64_t* ids, const int64_t* mask, int B, int L, int32_t* ids_out) const;
   BatchPlan plan_lens(const int32_t* h_lens, int B) const;
   void ensure_workspace(int Tb, int Bb);
@@ -189,9 +203,14 @@ class Engine {
   int D_ = 0, H_ = 0, Dh_ = 0, F_ = 0, V_ = 0, nlayers_ = 0, max_pos_ = 0;
   int n_act_ = 0, head_layers_ = 0, lora_r_ = 0, max_len_ = 0;
   float eps_ = 1e-5f;
+  int arch_ = ARCH_MODERNBERT;  // ModernBERT (DecisionModel) or BERT (SjModel)
+  int act_head_ = ACT_MLP;
+  int head_ff_ = 0, head_act_ = 2;
+  float head_eps_ = 1e-5f;
   bool use_graphs_ = true, pad_rows_ = false;
 
   DevBuf emb_w_, emb_norm_, final_norm_, type_emb_;
+  DevBuf pos_emb_, emb_norm_b_, final_norm_b_;  // BERT family
   DevBuf rope_cos_full_, rope_sin_full_, rope_cos_slide_, rope_sin_slide_;
   std::vector<LayerDev> layers_;
   std::vector<HeadDev> head_;

@@ -476,6 +476,34 @@ __global__ void act_softmax_kernel(const float* a, int B, int n, float* act) {
     act[static_cast<int64_t>(b) * n + j] = static_cast<float>(static_cast<double>(expf(ab[j] - amx)) / as);
 }
 
+// SjModel's act head (src/sj_model.cpp:336-367), one thread per row:
+// logits[b, k] = mmask[b, k] ? s2[b, k] : -1e4; p = softmax over the row's K
+// logits (float exp of the max-subtracted logit, double sum and division);
+// act[b] = {top1, 1 - top1}.
+__global__ void act_top1_kernel(const float* s2, const int* mmask, int B, int K, float* logits,
+                                float* act) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const float* sb = s2 + static_cast<int64_t>(b) * K;
+  const int* mb = mmask + static_cast<int64_t>(b) * K;
+  float* lg = logits + static_cast<int64_t>(b) * K;
+  float mx = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const float v = mb[k] ? sb[k] : -1e4f;
+    lg[k] = v;
+    mx = (k == 0 || v > mx) ? v : mx;
+  }
+  double s = 0.0;
+  for (int k = 0; k < K; ++k) s += static_cast<double>(expf(lg[k] - mx));
+  double top1 = 0.0;
+  for (int k = 0; k < K; ++k) {
+    const double p = static_cast<double>(expf(lg[k] - mx)) / s;
+    top1 = (k == 0 || p > top1) ? p : top1;
+  }
+  act[2 * b] = static_cast<float>(top1);
+  act[2 * b + 1] = static_cast<float>(1.0 - top1);
+}
+
 // Lengths of a batch, passed by value (no host staging buffer).
 struct SeqTableArgs {
   int B, Bb;
@@ -553,6 +581,13 @@ void launch_act_features(const float* s2, const int* mmask, int B, int K, const 
   if (B <= 0 || K <= 0) return;
   act_features_kernel<<<B, 256, 0, st>>>(s2, mmask, K, cls, ld_cls, D, logits, ain, ld_ain);
   check_launch("act_features");
+}
+
+void launch_act_top1(const float* s2, const int* mmask, int B, int K, float* logits, float* act,
+                     hipStream_t st) {
+  if (B <= 0 || K <= 0) return;
+  act_top1_kernel<<<(B + 63) / 64, 64, 0, st>>>(s2, mmask, B, K, logits, act);
+  check_launch("act_top1");
 }
 
 void launch_act_softmax(const float* a, int B, int n, float* act, hipStream_t st) {

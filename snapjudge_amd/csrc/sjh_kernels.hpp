@@ -160,6 +160,17 @@ void launch_token_index(const int* seq_start, const int* rows, int B, int* tok_p
 void launch_add_row_embedding(float* X, int64_t ldx, const float* table, const int* sel,
                               const int* tok_seq, int T, const int* T_dev, int D, hipStream_t st);
 
+// Checkpoint staging conversions (convert.hip), element types of the source:
+enum SrcType : int { SRC_F32 = 0, SRC_F16 = 1, SRC_BF16 = 2, SRC_F8 = 3 };
+// dst[i] = exact fp32 value of src[i] (bf16 or f16)
+void launch_widen_f32(const void* src, int src_dtype, float* dst, int64_t n, hipStream_t st);
+// dst[i] = bf16 nearest to src[i] (f32 or f16), ties to even
+void launch_narrow_bf16(const void* src, int src_dtype, uint16_t* dst, int64_t n, hipStream_t st);
+// Per-row e4m3 codes and scales of a [rows, cols] fp32 matrix, identical to
+// the host quantizer (sjh_quantize_fp8)
+void launch_quantize_fp8_rows(const float* w, int64_t rows, int64_t cols, uint8_t* q,
+                              float* scale, hipStream_t st);
+
 // Per-batch sequence table (device int32), for Bb >= B table entries:
 //   [0] total tokens T = sum of lens, [1] B, [2..3] 0,
 //   seq_start[Bb] at 4, q_len[Bb], k_len[Bb], qtype[Bb], order[Bb], then,
@@ -188,5 +199,9 @@ void launch_act_features(const float* s2, const int* mmask, int B, int K, const 
                          hipStream_t st);
 // act[b, :] = softmax(a[b, :n]) with the reference's float exp / double sums
 void launch_act_softmax(const float* a, int B, int n, float* act, hipStream_t st);
+// SjModel's act head (src/sj_model.cpp:336-367): masked logits as in
+// launch_act_features, then act[b, :] = {top1, 1 - top1} of their softmax
+void launch_act_top1(const float* s2, const int* mmask, int B, int K, float* logits, float* act,
+                     hipStream_t st);
 
 }  // namespace sjh

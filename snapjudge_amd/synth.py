@@ -240,6 +240,24 @@ def write_sj_checkpoint(path: str, cfg: dict, tensors: dict, store="F32") -> Non
     write_safetensors(os.path.join(path, "model.safetensors"), tensors, store)
 
 
+FP8_PROJECTIONS = ("attn.Wqkv.weight", "attn.Wo.weight", "mlp.Wi.weight", "mlp.Wo.weight")
+
+
+def fp8_tensors(tensors: dict, quantize) -> dict:
+    """The tensors of an SJH_PREC_FP8W checkpoint: each encoder projection as
+    ("F8_E4M3", codes) plus "<name>_scale" (fp32, one per row), from the given
+    per-row quantizer (snapjudge_amd.quantize_fp8); other tensors unchanged."""
+    out = {}
+    for k, v in tensors.items():
+        if k.startswith("encoder.layers.") and k.split(".", 3)[-1] in FP8_PROJECTIONS:
+            q, sc = quantize(v)
+            out[k] = ("F8_E4M3", q)
+            out[k + "_scale"] = ("F32", sc.astype(np.float32))
+        else:
+            out[k] = v
+    return out
+
+
 def read_checkpoint(path: str):
     """(rl_cfg, enc_cfg, tensors as fp32), widening F16/BF16 like
     src/safetensors.cpp:109-135."""
