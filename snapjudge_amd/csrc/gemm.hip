@@ -1180,6 +1180,13 @@ void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
 // of 128 x 64 (one workgroup per CU, 256 VGPRs per wave)
 #define SJH_GEMM_PERS_FP8 256, 256, 2, 4, 3, 64
 
+#ifndef SJH_GEMM_SMALL
+#define SJH_GEMM_SMALL 64, 64, 2, 1, 4, 64
+#endif
+#ifndef SJH_SPLITK_MAX_M
+#define SJH_SPLITK_MAX_M 256
+#endif
+
 // The persistent kernel's epilogues write 8- and 16-byte vectors, and its
 // loads address each operand by 32-bit byte offsets.
 bool pers_ok(const GemmArgs& g) {
@@ -1200,7 +1207,7 @@ void launch_mfma(const GemmArgs& g, hipStream_t st) {
   else if (g.M >= 1024)
     launch_mfma_epi<SJH_GEMM_MID>(g, st);
   else
-    launch_mfma_epi<64, 64, 2, 1, 4, 64>(g, st);
+    launch_mfma_epi<SJH_GEMM_SMALL>(g, st);
 }
 
 // ------------------------------------------------------------------ split-K
@@ -1402,7 +1409,7 @@ bool mfma_ok(const GemmArgs& g) {
 }
 
 int launch_gemm_resid_partials(const GemmArgs& g0, hipStream_t st) {
-  if (g0.epi != EPI_RESID || g0.M <= 0 || g0.M > 256 || g0.N <= 0 || g0.K <= 0 || !g0.partial ||
+  if (g0.epi != EPI_RESID || g0.M <= 0 || g0.M > SJH_SPLITK_MAX_M || g0.N <= 0 || g0.K <= 0 || !g0.partial ||
       !g0.A || !g0.W || !g0.X || g0.lda < g0.K || g0.ldw < g0.K || g0.ldx < g0.N || !mfma_ok(g0))
     return 0;
   GemmArgs g = g0;
@@ -1458,7 +1465,7 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
   // split-K only for the residual epilogue: its few output tiles (N = D)
   // leave most CUs idle otherwise; the wider products (QKV, GEGLU) have
   // enough tiles, and a second epilogue kernel costs more than it saves
-  if (mfma && g.partial && g.M <= 256 && g.epi == EPI_RESID && launch_splitk(g, st)) return;
+  if (mfma && g.partial && g.M <= SJH_SPLITK_MAX_M && g.epi == EPI_RESID && launch_splitk(g, st)) return;
   if (mfma) {
     launch_mfma(g, st);
     check_launch("gemm_bf16_mfma");
