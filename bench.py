@@ -33,7 +33,9 @@ forward replayed as a captured hipGraph).  Also reported:
                    same workload, extrapolated by layers;
   other_configs -- configs 4 (batch 4 x seq 8192) and 5 (28-layer/1024
                    encoder with fp8 e4m3 weights, batch 32 x seq 1024): valid
-                   tokens/s and per-kernel times, same method.
+                   tokens/s and per-kernel times, same method; for config 5
+                   also the decision step over 8 typed questions per sequence
+                   (256 rows, forward_shared, host arrays in and out).
 --legs selects the legs (default all: cfg3,b1,cfg4,cfg5,cpu); a run without
 cfg3 prints the other legs with a null value (profiling runs only).
 """
@@ -226,17 +228,61 @@ def encoder_leg(sj, torch, model, ids, lens, D, steps, warmup, stream):
     return elapsed * 1e3 / steps, T * steps / elapsed, prof
 
 
-def extra_leg(sj, torch, name, preset, precision, B, S, lo, hi, steps, stream):
-    """BASELINE config 4 or 5 (encoder tokens/s; not the headline line)."""
+QTYPE_MARKERS = {0: (4, 16), 1: (5, 5), 2: (2, 2)}  # choice K in [4, 16], score 5, noul 2
+
+
+def decision_leg(model, ids, mask, lens, n_q, steps, seed=3):
+    """Config 5's decision step: each of the U sequences carries n_q typed
+    questions (qtype uniform over choice / score / noul, src/common.cpp:12-13,
+    with the marker counts above), U * n_q rows through forward_shared: the
+    encoder on the U sequences, the head layers once per distinct (sequence,
+    qtype) pair, the scorer and act head per row.  Host arrays in, logits and
+    act out, as DecisionModel::forward's interface, so the time includes the
+    host<->device copies.  For comparison, the same rows through forward on
+    the U * n_q-row expansion (every row encoded and run through the head)."""
+    from snapjudge_amd import synth
+
+    rng = np.random.default_rng(seed)
+    U = len(lens)
+    row_seq = np.repeat(np.arange(U), n_q).astype(np.int32)
+    qt = rng.integers(0, 3, size=len(row_seq))
+    kinds = [(int(t), int(rng.integers(QTYPE_MARKERS[int(t)][0], QTYPE_MARKERS[int(t)][1] + 1)))
+             for t in qt]
+    mp, mm, qt = synth.make_markers(lens[row_seq], 16, kinds, seed=seed)
+    pairs = len({(int(u), int(t)) for u, t in zip(row_seq, qt)})
+
+    def timed(fn, n):
+        fn()  # warm-up: graph capture, workspace growth
+        t = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            t.append(time.perf_counter() - t0)
+        return float(np.median(t)) * 1e3
+
+    shared = timed(lambda: model.forward_shared(ids, mask, row_seq, mp, mm, qt), steps)
+    xi, xm = ids[row_seq], mask[row_seq]
+    expanded = timed(lambda: model.forward(xi, xm, mp, mm, qt), max(2, steps // 2))
+    rows = len(row_seq)
+    return {"rows": rows, "sequences": U, "head_pairs": pairs,
+            "forward_shared_ms": round(shared, 3), "rows_per_s": round(rows / (shared / 1e3), 1),
+            "expanded_forward_ms": round(expanded, 3),
+            "expanded_rows_per_s": round(rows / (expanded / 1e3), 1)}
+
+
+def extra_leg(sj, torch, name, preset, precision, B, S, lo, hi, steps, stream, questions=0):
+    """BASELINE config 4 or 5 (encoder tokens/s; not the headline line), and
+    with questions > 0 the decision step over that many questions per row."""
     from snapjudge_amd import synth
 
     rl, enc, w = synth.make_model(**synth.PRESETS[preset], seed=0)
     cfg = synth.flat_cfg(rl, enc)
     D, F, NL = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
-    ids, _, lens = synth.make_batch(B, S, lo, hi, cfg["vocab_size"], seed=1)
+    ids, mask, lens = synth.make_batch(B, S, lo, hi, cfg["vocab_size"], seed=1)
     model = sj.Model(w, cfg, precision=precision, use_graphs=True)
     del w
     ms, tps, prof = encoder_leg(sj, torch, model, ids, lens, D, steps, 2, stream)
+    decision = decision_leg(model, ids, mask, lens, questions, steps) if questions else None
     model.close()
     T = int(lens.sum())
     gemm_ms = sum(prof[n][0] for n in GEMM_NAMES if n in prof)
@@ -248,7 +294,8 @@ def extra_leg(sj, torch, name, preset, precision, B, S, lo, hi, steps, stream):
             "attention_tflops": kt["attention"]["achieved"] if "attention" in kt else None,
             "dominant_kernel": dom,
             "kernels": {g: {k: v for k, v in d.items() if k != "kernel"} for g, d in kt.items()},
-            "kernel_ms_per_step": {k: round(v[0] / steps, 4) for k, v in sorted(prof.items())}}
+            "kernel_ms_per_step": {k: round(v[0] / steps, 4) for k, v in sorted(prof.items())},
+            **({"decision": decision} if decision else {})}
 
 
 def b1_legs(sj, torch, w, cfg, stream):
@@ -393,7 +440,7 @@ def main():
         extra["cfg5"] = extra_leg(sj, torch, "BASELINE config 5: 28-layer/1024 encoder, GEGLU 2624, "
                                   "per-row fp8 e4m3 projection weights (bf16 activations), batch "
                                   "32 x seq 1024, lengths U[256,1024] seed 1", "cfg5",
-                                  sj.SJH_PREC_FP8W, 32, 1024, 256, 1024, 5, stream)
+                                  sj.SJH_PREC_FP8W, 32, 1024, 256, 1024, 5, stream, questions=8)
     cpu = cpu_baseline(w, rl, enc, ids, mask, lens, NL) if "cpu" in legs else None
     out = {
         "metric": METRIC, "value": round(value, 1) if value else None, "unit": "tokens/s",

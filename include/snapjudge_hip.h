@@ -152,6 +152,21 @@ int sjh_model_forward(sjh_model* m, const int64_t* ids, const int64_t* mask,
                       const int64_t* marker_pos, const uint8_t* marker_mask, const int64_t* qtype,
                       int32_t B, int32_t L, int32_t K, float* logits, float* act);
 
+/* DecisionModel::forward (src/model.cpp:309-536) on B rows that share U
+ * token sequences: row b reads sequence row_seq[b] of ids/mask [U, L], with
+ * its own marker_pos [B, K], marker_mask [B, K] and qtype [B].  The results
+ * are those of sjh_model_forward on the B-row batch ids[row_seq[b]] (the
+ * encoder depends on the tokens only, src/model.cpp:332-407).  Each sequence
+ * is encoded once; the head layers, whose input is the sequence plus the type
+ * embedding of the row's qtype (src/model.cpp:409-459), run once per distinct
+ * (sequence, qtype) pair, and the scorer and act head once per row.  The
+ * shape of 32 sequences x 8 typed questions: no counterpart in the
+ * reference, which runs the 256 rows through DecisionModel::forward. */
+int sjh_model_forward_shared(sjh_model* m, const int64_t* ids, const int64_t* mask, int32_t U,
+                             int32_t L, const int32_t* row_seq, const int64_t* marker_pos,
+                             const uint8_t* marker_mask, const int64_t* qtype, int32_t B,
+                             int32_t K, float* logits, float* act);
+
 /* Encoder on a batch already resident in device memory: d_ids [T] int32 holds
  * the B sequences back to back, h_lens [B] (host) their lengths, T = sum.
  * Writes the final hidden states [T, D] fp32 to d_hidden.  Work is enqueued on

@@ -72,6 +72,8 @@ _SIGS = {
                                     C.c_int32, C.c_int32, _fp, _fp]),
     "sjh_model_encode_device": (C.c_int, [C.c_void_p, C.c_void_p, _i32p, C.c_int32, C.c_void_p,
                                           C.c_void_p]),
+    "sjh_model_forward_shared": (C.c_int, [C.c_void_p, _i64p, _i64p, C.c_int32, C.c_int32, _i32p,
+                                           _i64p, _u8p, _i64p, C.c_int32, C.c_int32, _fp, _fp]),
     "sjh_model_encode_device_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, _i32p, C.c_int32,
                                                   C.c_void_p, C.c_void_p]),
     "sjh_model_info": (C.c_int, [C.c_void_p, _i32p, _i32p, _i32p, _i32p]),
@@ -289,6 +291,27 @@ class Model:
                                       mp.ctypes.data_as(_i64p), mm.ctypes.data_as(_u8p),
                                       qt.ctypes.data_as(_i64p), B, L, K,
                                       logits.ctypes.data_as(_fp), act.ctypes.data_as(_fp)))
+        return logits, act
+
+    def forward_shared(self, ids, mask, row_seq, marker_pos, marker_mask, qtype):
+        """forward on len(row_seq) rows; row b is sequence row_seq[b] of ids/mask."""
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        mask = np.ascontiguousarray(mask, dtype=np.int64)
+        rs = np.ascontiguousarray(row_seq, dtype=np.int32)
+        mp = np.ascontiguousarray(marker_pos, dtype=np.int64)
+        mm = np.ascontiguousarray(marker_mask, dtype=np.uint8)
+        qt = np.ascontiguousarray(qtype, dtype=np.int64)
+        U, L = ids.shape
+        B, K = mp.shape
+        assert len(rs) == B and mm.shape == (B, K) and len(qt) == B
+        logits = np.empty((B, K), dtype=np.float32)
+        act = np.empty((B, self.n_act), dtype=np.float32)
+        check(lib().sjh_model_forward_shared(self._h, ids.ctypes.data_as(_i64p),
+                                             mask.ctypes.data_as(_i64p), U, L,
+                                             rs.ctypes.data_as(_i32p), mp.ctypes.data_as(_i64p),
+                                             mm.ctypes.data_as(_u8p), qt.ctypes.data_as(_i64p),
+                                             B, K, logits.ctypes.data_as(_fp),
+                                             act.ctypes.data_as(_fp)))
         return logits, act
 
     def encode_device(self, d_ids: int, lens: np.ndarray, d_hidden: int, stream: int = 0):

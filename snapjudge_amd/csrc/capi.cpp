@@ -140,6 +140,18 @@ int sjh_model_forward(sjh_model* m, const int64_t* ids, const int64_t* mask,
   });
 }
 
+int sjh_model_forward_shared(sjh_model* m, const int64_t* ids, const int64_t* mask, int32_t U,
+                             int32_t L, const int32_t* row_seq, const int64_t* marker_pos,
+                             const uint8_t* marker_mask, const int64_t* qtype, int32_t B,
+                             int32_t K, float* logits, float* act) {
+  return guarded([&] {
+    if (!m) sjh::fail("null model");
+    if (B < 0 || U < 0) sjh::fail("negative batch");
+    m->eng->forward_shared(ids, mask, U, L, row_seq, marker_pos, marker_mask, qtype, B, K, logits,
+                           act);
+  });
+}
+
 int sjh_model_encode_device(sjh_model* m, const int32_t* d_ids, const int32_t* h_lens, int32_t B,
                             float* d_hidden, sjh_stream_t stream) {
   return guarded([&] {

@@ -1409,19 +1409,118 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
     qt[static_cast<size_t>(b)] = static_cast<int32_t>(qtype[b]);
   }
   ensure_workspace(p.Tb, p.Bb);
-  const int D = D_;
   hipStream_t st = stream_;
   begin_call(st);
   if (p.T > 0) {
     upload_batch(p, packed.data(), qt.data(), st);
     run_device_maybe_graph(p, ids_.as<int32_t>(), X_.as<float>(), true, st);
   }
+  decision_tail(p, X_.as<float>(), marker_pos, marker_mask, L, K, logits, act, st);
+  end_call(st);
+  hip_check(hipStreamSynchronize(st), "forward: decision head");
+  if (profile_) prof_collect();
+}
 
+void Engine::forward_shared(const int64_t* ids, const int64_t* mask, int U, int L,
+                            const int32_t* row_seq, const int64_t* marker_pos,
+                            const uint8_t* marker_mask, const int64_t* qtype, int B, int K,
+                            float* logits, float* act) {
+  std::lock_guard<std::mutex> lk(mu_);
+  hip_check(hipSetDevice(dev_), "hipSetDevice");
+  if (B <= 0) return;
+  require(U > 0, "forward_shared: need at least one sequence");
+  require(ids && mask && row_seq && marker_pos && marker_mask && qtype && logits && act,
+          "forward_shared: null argument");
+  require(K > 0, "forward_shared: need at least one marker column");
+  // the U sequences, encoded once
+  BatchPlan p0 = plan(ids, mask, U, L, nullptr);
+  std::vector<int32_t> packed(static_cast<size_t>(p0.T));
+  BatchPlan pu = plan(ids, mask, U, L, packed.data());
+  // The head's input for row b is sequence row_seq[b]'s hidden states plus
+  // the type embedding of qtype[b] (src/model.cpp:409-459); the markers enter
+  // only in the tail.  Rows that share (sequence, qtype) are therefore
+  // identical through the head layers, which run once per distinct pair: pe
+  // holds the pairs, pt the B rows, each pointing at its pair's rows.
+  BatchPlan pe, pt;
+  pe.L = pt.L = L;
+  pt.B = B;
+  pt.seq_start.resize(static_cast<size_t>(B));
+  pt.q_len.resize(static_cast<size_t>(B));
+  std::vector<int32_t> qt, pair_seq;
+  std::vector<int32_t> pair_of(static_cast<size_t>(U) * 3, -1);
+  int64_t T = 0;
+  for (int b = 0; b < B; ++b) {
+    const int u = row_seq[b];
+    if (u < 0 || u >= U) fail("forward_shared: row_seq outside [0, U)");
+    if (qtype[b] < 0 || qtype[b] > 2) fail("qtype must be 0, 1 or 2");
+    int32_t& j = pair_of[static_cast<size_t>(u) * 3 + static_cast<size_t>(qtype[b])];
+    if (j < 0) {
+      j = static_cast<int32_t>(qt.size());
+      qt.push_back(static_cast<int32_t>(qtype[b]));
+      pair_seq.push_back(u);
+      const int n = pu.q_len[static_cast<size_t>(u)];
+      pe.seq_start.push_back(static_cast<int32_t>(T));
+      pe.q_len.push_back(n);
+      pe.k_len.push_back(pu.k_len[static_cast<size_t>(u)]);
+      pe.max_q = std::max(pe.max_q, n);
+      T += n;
+    }
+    pt.seq_start[static_cast<size_t>(b)] = pe.seq_start[static_cast<size_t>(j)];
+    pt.q_len[static_cast<size_t>(b)] = pe.q_len[static_cast<size_t>(j)];
+  }
+  if (T > (int64_t{1} << 30)) fail("batch too large");
+  pe.B = static_cast<int>(qt.size());
+  pe.T = static_cast<int>(T);
+  set_order(pe);
+  set_bucket(pe);
+  // the source row of every head token
+  std::vector<int32_t> src(static_cast<size_t>(pe.T));
+  for (int j = 0; j < pe.B; ++j) {
+    const int u = pair_seq[static_cast<size_t>(j)];
+    for (int i = 0; i < pe.q_len[static_cast<size_t>(j)]; ++i)
+      src[static_cast<size_t>(pe.seq_start[static_cast<size_t>(j)] + i)] =
+          pu.seq_start[static_cast<size_t>(u)] + i;
+  }
+  ensure_workspace(std::max(pu.Tb, pe.Tb), std::max(pu.Bb, pe.Bb));
+  const size_t D = D_;
+  X2_.ensure(std::max<size_t>(static_cast<size_t>(pe.Tb) * D * 4, 4));
+  expand_idx_.ensure(std::max<size_t>(src.size() * 4, 4));
+  hipStream_t st = stream_;
+  begin_call(st);
+  if (pu.T > 0) {
+    upload_batch(pu, packed.data(), nullptr, st);
+    run_device_maybe_graph(pu, ids_.as<int32_t>(), X_.as<float>(), false, st);
+  }
+  if (pe.T > 0) {
+    // after the encoder (same stream): the pairs' table, their hidden states
+    // gathered from the encoded sequences, then the head layers
+    upload_batch(pe, nullptr, qt.data(), st);
+    hip_check(hipMemcpyAsync(expand_idx_.get(), src.data(), src.size() * 4, hipMemcpyHostToDevice, st),
+              "upload expanded rows");
+    launch_gather_rows(X_.as<float>(), D_, expand_idx_.as<int32_t>(), pe.T, D_, X2_.as<float>(), D_,
+                       st);
+    launch_token_index(ws_.seq + kSeqHdr, ws_.seq + kSeqHdr + pe.Bb, pe.Bb, ws_.tok_pos, ws_.tok_seq,
+                       st);
+    enqueue_head_layers(pe, ws_, X2_.as<float>(), st);
+  }
+  decision_tail(pt, X2_.as<float>(), marker_pos, marker_mask, L, K, logits, act, st);
+  end_call(st);
+  hip_check(hipStreamSynchronize(st), "forward_shared: decision head");
+  if (profile_) prof_collect();
+}
+
+void Engine::decision_tail(const BatchPlan& p, const float* X, const int64_t* marker_pos,
+                           const uint8_t* marker_mask, int L, int K, float* logits, float* act,
+                           hipStream_t st) {
+  const int B = p.B, D = D_;
   // ---- scorer (src/model.cpp:461-487) and act head (:489-535), all on the
   // device: gather the marker rows and the [CLS] rows, then only the logits
   // and the act probabilities come back
   const int nmk = B * K, nrow = nmk + B;
-  std::vector<int32_t> idx(static_cast<size_t>(nrow + nmk));  // row indices, then the marker mask
+  // row indices, then the marker mask; a member, so that it outlives the
+  // copy below until the caller synchronizes
+  std::vector<int32_t>& idx = tail_hidx_;
+  idx.assign(static_cast<size_t>(nrow + nmk), 0);
   for (int b = 0; b < B; ++b) {
     for (int k = 0; k < K; ++k) {
       int64_t pp = marker_pos[static_cast<int64_t>(b) * K + k];
@@ -1448,7 +1547,7 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
   tail_act_.ensure(static_cast<size_t>(B) * n_act_ * 4);
   hip_check(hipMemcpyAsync(tail_idx_.get(), idx.data(), idx.size() * 4, hipMemcpyHostToDevice, st),
             "upload marker rows");
-  launch_gather_rows(X_.as<float>(), D, tail_idx_.as<int32_t>(), nrow, D, tail_rows_.as<float>(),
+  launch_gather_rows(X, D, tail_idx_.as<int32_t>(), nrow, D, tail_rows_.as<float>(),
                      D, st);
   {
     LnArgs a;
@@ -1533,9 +1632,6 @@ void Engine::forward(const int64_t* ids, const int64_t* mask, const int64_t* mar
   hip_check(hipMemcpyAsync(act, tail_act_.get(), static_cast<size_t>(B) * n_act_ * 4,
                            hipMemcpyDeviceToHost, st),
             "download act");
-  end_call(st);
-  hip_check(hipStreamSynchronize(st), "forward: decision head");
-  if (profile_) prof_collect();
 }
 
 }  // namespace sjh

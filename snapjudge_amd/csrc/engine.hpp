@@ -117,6 +117,12 @@ class Engine {
                float* logits, float* act);
   void encode_device(const int32_t* d_ids, const int32_t* h_lens, int B, float* d_hidden,
                      hipStream_t stream);
+  // forward on B rows that share U token sequences: row b is sequence
+  // row_seq[b] of ids/mask [U, L] with its own markers and qtype
+  void forward_shared(const int64_t* ids, const int64_t* mask, int U, int L,
+                      const int32_t* row_seq, const int64_t* marker_pos,
+                      const uint8_t* marker_mask, const int64_t* qtype, int B, int K,
+                      float* logits, float* act);
   // encode_device with every buffer carved out of the library's fixed
   // per-device scratch array: no device allocation, no graph, no pinned
   // staging.  Throws when the batch does not fit the array.
@@ -173,6 +179,10 @@ class Engine {
   void enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_ids, float* X,
                        hipStream_t st);
   void enqueue_head_layers(const BatchPlan& p, const Ws& w, float* X, hipStream_t st);
+  // scorer and act head on the final hidden states X of plan p (src/model.cpp:461-535)
+  void decision_tail(const BatchPlan& p, const float* X, const int64_t* marker_pos,
+                     const uint8_t* marker_mask, int L, int K, float* logits, float* act,
+                     hipStream_t st);
   // order this call's stream after the engine's previous call (any stream),
   // and mark the end of this call's work
   void begin_call(hipStream_t st);
@@ -222,6 +232,8 @@ class Engine {
   int cap_T_ = 0, cap_B_ = 0;
   DevBuf ids_, seqinfo_, tok_pos_, tok_seq_;
   DevBuf X_, Y_, QKV_, O_, G_, Z_;
+  DevBuf X2_, expand_idx_;  // forward_shared: hidden states of the (sequence, qtype) pairs
+  std::vector<int32_t> tail_hidx_;  // host copy of the head tail's row indices
   DevBuf splitk_;  // split-K partial sums for short batches (GemmArgs::partial)
   Ws ws_;          // views of the buffers above
   DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_lg_, tail_ain_, tail_ah_,
