@@ -94,18 +94,27 @@ KERNEL_GROUPS = {
 }
 
 
+def role_work(role, T, D, F, sum_n2):
+    """Algorithmic work of one launch of an event role: (FLOPs, HBM bytes) over
+    valid tokens -- every operand read once, every output written once."""
+    return {
+        "gemm_qkv_rope": (2.0 * T * D * 3 * D, 2.0 * (T * D + 3 * D * D + 3 * T * D)),
+        "gemm_wi_geglu": (2.0 * T * D * 2 * F, 2.0 * (T * D + 2 * F * D + T * F)),
+        "gemm_wo_resid": (2.0 * T * D * D, 2.0 * (T * D + D * D) + 8.0 * T * D),
+        "gemm_wo2_resid": (2.0 * T * F * D, 2.0 * (T * F + D * F) + 8.0 * T * D),
+        "attention": (4.0 * D * sum_n2, 8.0 * T * D),
+        "attn_norm": (0.0, 6.0 * T * D),
+        "mlp_norm": (0.0, 6.0 * T * D),
+        "final_norm": (0.0, 8.0 * T * D),
+    }[role]
+
+
 def kernel_table(prof, steps, T, D, F, NL, lens):
     """Per kernel group: launches and ms per step, mean launch time, and the
-    algorithmic rate against its roofline.  Work per launch (valid tokens):
-    QKV 2*T*D*3D, GEGLU 2*T*D*2F, residual (Wo, Wo2 mean) 2*T*(D*D + F*D)/2,
-    attention 4*D*sum(n^2), layer norm bytes 6*T*D (fp32 read, bf16 write;
-    the final norm writes fp32 rows: 8*T*D)."""
+    algorithmic rate against its roofline (MFMA FLOPs for the GEMMs and
+    attention, HBM bytes for the layer norms), with the other rate beside it.
+    Work per launch is role_work's, averaged over the group's launches."""
     sum_n2 = float((lens.astype(np.float64) ** 2).sum())
-    total = {"gemm_qkv_rope": 2.0 * T * D * 3 * D * NL,
-             "gemm_wi_geglu": 2.0 * T * D * 2 * F * NL,
-             "gemm_resid": 2.0 * T * (D * D + F * D) * NL,
-             "attention": 4.0 * D * sum_n2 * NL,
-             "layer_norm": None}
     out = {}
     for grp, (roles, kname, bound) in KERNEL_GROUPS.items():
         ms = sum(prof[r][0] for r in roles if r in prof)
@@ -113,21 +122,19 @@ def kernel_table(prof, steps, T, D, F, NL, lens):
         if n == 0:
             continue
         per_step = n // steps
-        if grp == "layer_norm":
-            n_final = prof.get("final_norm", (0.0, 0))[1] // steps
-            work_step = (6.0 * (per_step - n_final) + 8.0 * n_final) * T * D
-        else:
-            work_step = total[grp]
+        flops = sum(role_work(r, T, D, F, sum_n2)[0] * prof[r][1] for r in roles if r in prof) / n
+        nbytes = sum(role_work(r, T, D, F, sum_n2)[1] * prof[r][1] for r in roles if r in prof) / n
         avg_s = ms / 1e3 / n
-        rate = work_step / per_step / avg_s  # per launch / s
+        tflops, gbs = flops / avg_s / 1e12, nbytes / avg_s / 1e9
         peak = PEAK_HBM_GBS if bound == "hbm" else PEAK_BF16_TFLOPS
-        achieved = rate / 1e9 if bound == "hbm" else rate / 1e12
+        achieved = gbs if bound == "hbm" else tflops
         out[grp] = {"kernel": kname, "bound": bound, "launches_per_step": per_step,
                     "ms_per_step": round(ms / steps, 4), "avg_launch_us": round(avg_s * 1e6, 3),
-                    "work_per_launch": work_step / per_step,
+                    "work_per_launch": flops if bound == "mfma" else nbytes,
                     "achieved": round(achieved, 2), "peak": peak,
                     "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
-                    "frac": round(achieved / peak, 4)}
+                    "frac": round(achieved / peak, 4),
+                    "tflops": round(tflops, 2), "hbm_gbs": round(gbs, 1)}
     return out
 
 

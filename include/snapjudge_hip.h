@@ -268,6 +268,14 @@ int sjh_rope(void* qkv, const float* cos_t, const float* sin_t, int64_t M, int32
 int sjh_attn(const void* qkv, const int32_t* lens, void* O, int32_t B, int32_t L, int32_t H,
              int32_t Dh, int32_t window, int32_t dtype, sjh_stream_t stream);
 
+/* sjh_attn on queries that already hold q * (1/sqrt(64)) * log2(e), bf16 with
+ * head_dim 64: the layout the encoder's QKV projection writes (the scale is
+ * folded into the projection's epilogue, so the QK^T product yields log2-
+ * domain logits).  Same masking and output as sjh_attn.  No counterpart in the
+ * reference, which scales the scores (src/tensor.cpp:186-200). */
+int sjh_attn_log2(const void* qkv, const int32_t* lens, void* O, int32_t B, int32_t L, int32_t H,
+                  int32_t window, sjh_stream_t stream);
+
 /* Embedding gather + LayerNorm (src/model.cpp:332-340): X[r] = LN(table[ids[r]]) * w.
  * table [V, D] of dtype, ids int32 [M], X fp32 [M, D]. */
 int sjh_embed_ln(const void* table, const int32_t* ids, const float* w, float* X, int32_t M,

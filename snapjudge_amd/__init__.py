@@ -100,6 +100,8 @@ _SIGS = {
                            C.c_int32, C.c_int32, C.c_void_p]),
     "sjh_attn": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
                            C.c_int32, C.c_int32, C.c_int32, C.c_void_p]),
+    "sjh_attn_log2": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                C.c_int32, C.c_void_p]),
     "sjh_embed_ln": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
                                C.c_int32, C.c_float, C.c_int32, C.c_void_p]),
 }

@@ -38,6 +38,13 @@ constexpr int kQ = 128;     // queries per workgroup (4 waves x 32)
 constexpr int kKey = 64;    // keys per tile
 constexpr int kNS = 2;      // LDS ring stages (2 x 16 KB)
 constexpr float kLazy = 8.f;  // log2 headroom before the running max is raised
+// Pre-scaled queries (q already times scale * log2 e, so the QK^T MFMA gives
+// log2-domain logits): the offset subtracted before exp2 is 0 whenever the
+// tile's max lies in [kZeroLo, kZeroHi] and is otherwise raised lazily with
+// kLazyPre of headroom; with a zero offset the exp2 argument is the MFMA
+// result itself (no multiply-add per logit).  exp2 of up to 2^32 and a sum
+// of 8192 such terms times V stay far inside fp32 and bf16 range.
+constexpr float kLazyPre = 32.f, kZeroLo = -64.f, kZeroHi = 32.f;
 constexpr int kStage = 2 * kKey * 128;  // bytes per stage: K tile then V tile, 64 x 128 B each
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
@@ -70,7 +77,9 @@ __device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
 
 // Register budget for three workgroups per CU (168 VGPRs, 3 waves per SIMD):
 // a third wave per SIMD lets softmax VALU work, MFMAs and LDS reads of
-// different waves overlap.
+// different waves overlap.  PRE: q holds q * scale * log2 e (AttnArgs::
+// q_log2_scaled).
+template <bool PRE>
 __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kNS * kStage];
   // Workgroup -> (sequence, head, query block).  Hardware hands workgroup i
@@ -175,7 +184,7 @@ __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
   // l_i: this lane's share of the softmax denominator, summed from the same
   // bf16 weights the P.V MFMA consumes (two partial sums, v_dot2 with ones)
   float m_i = -INFINITY, l_i = 0.f, l_j = 0.f;
-  const float c = a.scale * kLog2e;
+  const float c = PRE ? 1.f : a.scale * kLog2e;
 
   // LDS offsets (within a stage) of this lane's operand reads, the same for
   // every tile.  K fragments: row jb*32 + l32, dims 16*st + 8*hb + [0, 8).
@@ -231,17 +240,19 @@ __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
     // its running max m_i unless the tile's max exceeds it by more than
     // kLazy: p = 2^(s*c - m_i) then stays below 2^kLazy, the final 1/l
     // normalisation uses the same m_i, so the result is exact while the
-    // rescale of O and l is skipped for most tiles.
+    // rescale of O and l is skipped for most tiles.  PRE: the same with the
+    // offset held at 0 while the logits stay near 0 (kZeroLo, kZeroHi).
     float tmax = -INFINITY;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[jb][e]);
     tmax = wave_max32(tmax) * c;
-    const bool bump = tmax > m_i + kLazy;
+    const bool bump = tmax > m_i + (PRE ? kLazyPre : kLazy);
     if (__any(bump)) {
       asm volatile("" ::: "memory");  // keep this a branch (rarely taken), not a select
-      const float m_new = bump ? tmax : m_i;
+      const float m_tgt = PRE && tmax >= kZeroLo && tmax <= kZeroHi ? 0.f : tmax;
+      const float m_new = bump ? m_tgt : m_i;
       const float alpha = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_new);
       m_i = m_new;
       l_i *= alpha;
@@ -253,12 +264,26 @@ __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
       }
     }
     const float m_use = m_i == -INFINITY ? 0.f : m_i;
+    if constexpr (PRE) {
+      // the logits are already in the log2 domain; the offset is 0 for the
+      // whole wave unless a lane's logits left [kZeroLo, kZeroHi]
+      if (__any(m_use != 0.f)) {
+        asm volatile("" ::: "memory");  // a branch (rarely taken), not a select
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
+        for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s[jb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jb][e], c, -m_use));
+          for (int e = 0; e < 16; ++e) s[jb][e] -= m_use;
       }
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[jb][e] = __builtin_amdgcn_exp2f(s[jb][e]);
+    } else {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[jb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jb][e], c, -m_use));
+    }
     // O^T[dim][query] += V^T[dim][key] . P^T[key][query].  The MFMA's k index
     // 8 * hb + t of a 16-key step u stands for key 16u + 4hb + t (t < 4) or
     // 16u + 8 + 4hb + (t - 4): the order in which the S^T accumulator holds
@@ -453,10 +478,14 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
     const int64_t pairs8 = (static_cast<int64_t>(a.H) * a.B + 7) / 8 * 8;
     const int64_t nwg = pairs8 * ((a.max_q + kQ - 1) / kQ);
     require(nwg < (int64_t{1} << 31), "attention: too many workgroups");
-    attn_bf16_mfma_kernel<<<dim3(static_cast<unsigned>(nwg)), dim3(256), 0, st>>>(a);
+    if (a.q_log2_scaled)
+      attn_bf16_mfma_kernel<true><<<dim3(static_cast<unsigned>(nwg)), dim3(256), 0, st>>>(a);
+    else
+      attn_bf16_mfma_kernel<false><<<dim3(static_cast<unsigned>(nwg)), dim3(256), 0, st>>>(a);
     check_launch("attn_bf16_mfma");
     return;
   }
+  require(!a.q_log2_scaled, "attention: pre-scaled queries need the bf16 head_dim-64 kernel");
   if (a.dtype == DT_BF16)
     launch_generic<bf16_t>(a, st);
   else

@@ -407,6 +407,32 @@ int sjh_attn(const void* qkv, const int32_t* lens, void* O, int32_t B, int32_t L
   });
 }
 
+int sjh_attn_log2(const void* qkv, const int32_t* lens, void* O, int32_t B, int32_t L, int32_t H,
+                  int32_t window, sjh_stream_t stream) {
+  return guarded([&] {
+    if (L <= 0 || H <= 0) sjh::fail("attn_log2: bad shape");
+    const int64_t HD = static_cast<int64_t>(H) * 64;
+    sjh::AttnArgs a;
+    a.q = qkv;
+    a.k = static_cast<const char*>(qkv) + HD * 2;
+    a.v = static_cast<const char*>(qkv) + 2 * HD * 2;
+    a.ld_q = a.ld_k = a.ld_v = 3 * HD;
+    a.o = O;
+    a.ld_o = HD;
+    a.dtype = sjh::DT_BF16;
+    a.k_len = lens;
+    a.uniform_L = L;
+    a.B = B;
+    a.H = H;
+    a.Dh = 64;
+    a.max_q = L;
+    a.window = window;
+    a.scale = 0.125f;
+    a.q_log2_scaled = true;
+    sjh::launch_attn(a, as_stream(stream));
+  });
+}
+
 int sjh_embed_ln(const void* table, const int32_t* ids, const float* w, float* X, int32_t M,
                  int32_t D, float eps, int32_t dtype, sjh_stream_t stream) {
   return guarded([&] {

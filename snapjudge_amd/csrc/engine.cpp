@@ -865,6 +865,10 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
   }
 
   const float scale = 1.0f / std::sqrt(static_cast<float>(Dh_));
+  // bf16 with head_dim 64: the QKV projection writes q * scale * log2(e), so
+  // attention's QK^T product yields log2-domain logits (no per-logit scaling
+  // in its softmax); the rounding to bf16 then applies to the scaled q
+  const bool q_pre = !bert && adt == DT_BF16 && Dh_ == 64;
   // Y = attn_norm(X) of layer li (src/model.cpp:347-353; identity copy when
   // the layer has none)
   auto attn_norm_args = [&](int li) {
@@ -931,6 +935,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
         g.rope_rows = max_pos_;
         g.rope_dim = D;
         g.head_dim = Dh_;
+        if (q_pre) g.q_scale = scale * 1.4426950408889634f;
         gemm("gemm_qkv_rope", g, w, st);
       }
     }
@@ -954,6 +959,7 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       a.max_q = p.max_qb;
       a.window = ly.window;
       a.scale = scale;
+      a.q_log2_scaled = q_pre;
       attn("attention", a, st);
     }
     {  // X += O . Wo^T (src/model.cpp:389-391)

@@ -68,6 +68,7 @@ __device__ __forceinline__ void tile_epilogue(const float* Cs, int ldcs, int m0,
           const float cs = g.rope_cos[p * half + d2], sn = g.rope_sin[p * half + d2];
           v = rope_hi(x0, v, cs, sn);
         }
+        if (n < g.rope_dim) v *= g.q_scale;
       }
     } else {
       if (g.bias) v += g.bias[n];
@@ -295,6 +296,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
                 const float r1 = rope_hi(x0, x1, cs[e], sn[e]);
                 x0 = r0;
                 x1 = r1;
+                if (c0 + j * 32 < g.rope_dim) {  // a q head: attention's scale folded in
+                  x0 *= g.q_scale;
+                  x1 *= g.q_scale;
+                }
               }
               store_f32(reinterpret_cast<OutT*>(orow + j * 32 * EB), x0);
               if (!decltype(checked)::value || col + 32 < g.N) store_f32(reinterpret_cast<OutT*>(orow + (j + 1) * 32 * EB), x1);
@@ -629,6 +634,10 @@ __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)
               const float r1 = rope_hi(x0[t], x1[t], cs[q][t], sn[q][t]);
               x0[t] = r0;
               x1[t] = r1;
+              if (tile_n * BN + wn * WN + j * 32 < g.rope_dim) {  // a q head
+                x0[t] *= g.q_scale;
+                x1[t] *= g.q_scale;
+              }
             }
           }
           store4(orow + j * 32 + 8 * q, x0[0], x0[1], x0[2], x0[3]);
@@ -1249,6 +1258,7 @@ __device__ void splitk_output(const GemmArgs& g, int S, int m, int n) {
         v = rope_hi(splitk_sum(g, S, m, n - half), v, g.rope_cos[p * half + d - half],
                     g.rope_sin[p * half + d - half]);
       }
+      if (n < g.rope_dim) v *= g.q_scale;
     }
   } else {
     if (g.bias) v += g.bias[n];

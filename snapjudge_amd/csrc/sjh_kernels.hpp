@@ -52,6 +52,9 @@ struct GemmArgs {
   int rope_rows = 0;                // positions are clamped to [0, rope_rows)
   int rope_dim = 0;                 // D: columns [0, 2D) are q and k
   int head_dim = 0;
+  // ROPE: the rotated q columns [0, rope_dim) are multiplied by q_scale
+  // before the output rounding (attention's scale * log2 e, folded in)
+  float q_scale = 1.f;
   // Optional split-K workspace for short batches (M <= 256): partial sums of
   // K slices go to partial[split][M][N_w] (fp32) and a second kernel adds them
   // in split order and applies the epilogue.  Unused when null or too small.
@@ -142,6 +145,10 @@ struct AttnArgs {
   int uniform_L = 0;
   int window = 0;
   float scale = 0.f;  // 1/sqrt(Dh)
+  // q already holds q * scale * log2(e) (GemmArgs::q_scale of the QKV
+  // projection): the logits come out of the QK^T product in the log2 domain.
+  // bf16 with head_dim 64 only.
+  bool q_log2_scaled = false;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);
 

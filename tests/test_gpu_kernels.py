@@ -201,6 +201,41 @@ def test_attention_reference_layout(orc, dtype, Dh, window):
     assert float(np.abs(got - want).max()) <= tol
 
 
+@pytest.mark.parametrize("case", ["plain", "window", "large", "negative", "long"])
+def test_attention_log2_scaled_queries(orc, case):
+    # the encoder's layout: q pre-multiplied by scale * log2(e) before its bf16
+    # rounding.  "large" logits (std 20) raise the softmax offset above zero,
+    # "negative" ones (all below -64 in log2 units) start it below; "long"
+    # rows cross many key tiles
+    print(f"attn log2 {case}", flush=True)
+    B, L, H, Dh = 3, 1100 if case == "long" else 150, 2, 64
+    lens = [L, 71, 1] if case != "long" else [L, 700, 64]
+    rng = np.random.default_rng(len(case))
+    qkv = rnd(rng, (B, L, 3, H, Dh))
+    if case == "large":
+        qkv[:, :, 0] *= 20.0
+    if case == "negative":
+        qkv[:, :, 0, :, -1] = -40.0
+        qkv[:, :, 1, :, -1] = 10.0
+    window = 40 if case == "window" else 0
+    c = (1.0 / math.sqrt(Dh)) * math.log2(math.e)
+    pre = qkv.copy()
+    pre[:, :, 0] = bf16_round((qkv[:, :, 0].astype(np.float64) * c).astype(np.float32))
+    Q = dev(pre.reshape(B * L, 3 * H * Dh), torch.bfloat16)
+    Lens = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    O = torch.full((B * L, H * Dh), 7.0, dtype=torch.bfloat16, device="cuda")
+    call(sj.lib().sjh_attn_log2, P(Q), P(Lens), P(O), B, L, H, window, stream())
+    # the reference on the queries the kernel received (the pre-scaled bf16
+    # values divided by the scale), so the check does not also measure the
+    # bf16 rounding of q * c, which the encoder applies instead of that of q
+    qe = (pre[:, :, 0].astype(np.float64) / c).astype(np.float32)
+    q = np.ascontiguousarray(qe.transpose(0, 2, 1, 3))
+    k, v = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in (1, 2))
+    want = orc.attention(q, k, v, np.array(lens, np.int64), window)
+    want = want.transpose(0, 2, 1, 3).reshape(B * L, H * Dh)
+    assert float(np.abs(host(O) - want).max()) <= 2e-2
+
+
 def test_attention_long_context_sampled_rows():
     # S = 8192: check sampled query rows against a float64 reference of just those rows
     B, L, H, Dh = 2, 8192, 2, 64
