@@ -79,36 +79,11 @@ __device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
 // a third wave per SIMD lets softmax VALU work, MFMAs and LDS reads of
 // different waves overlap.  PRE: q holds q * scale * log2 e (AttnArgs::
 // q_log2_scaled).
+// One work item: queries [q0, q0 + kQ) of head h of the sequence whose rows
+// start at row0 (q0 < qlen).
 template <bool PRE>
-__global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kNS * kStage];
-  // Workgroup -> (sequence, head, query block).  Hardware hands workgroup i
-  // to XCD i % 8.  The (sequence, head) pairs, in seq_order's order, go to the
-  // XCDs round-robin, and an XCD's workgroups take its pairs' query blocks in
-  // turn, so the blocks of one pair run on one XCD close together and share
-  // its L2 for the pair's K/V tiles.
-  const int nblk = (a.max_q + kQ - 1) / kQ;
-  const int xcd = blockIdx.x & 7, kx = blockIdx.x >> 3;
-  const int pair = xcd + 8 * (kx / nblk);
-  if (pair >= a.H * a.B) return;  // uniform over the workgroup
-  const int zs = pair / a.H, h = pair - zs * a.H;
-  int qlen, klen;
-  int64_t row0;
-  if (a.seq_meta) {
-    const int4 m = reinterpret_cast<const int4*>(a.seq_meta)[zs];
-    row0 = m.x;
-    qlen = m.y;
-    klen = m.z;
-  } else {
-    const int b = a.seq_order ? a.seq_order[zs] : zs;
-    qlen = a.q_len ? a.q_len[b] : a.uniform_L;
-    // keys never extend past the rows a sequence owns (a caller's k_len > L
-    // in the padded layout is clamped rather than read out of bounds)
-    klen = a.seq_start ? a.k_len[b] : max(0, min(a.k_len[b], a.uniform_L));
-    row0 = a.seq_start ? a.seq_start[b] : static_cast<int64_t>(b) * a.uniform_L;
-  }
-  const int q0 = (kx % nblk) * kQ;
-  if (q0 >= qlen) return;  // uniform over the workgroup
+__device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t row0, int qlen, int klen,
+                                          int h, int q0) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hb = lane >> 5;
 
@@ -353,6 +328,76 @@ __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
   }
 }
 
+template <bool PRE>
+__global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kNS * kStage];
+  if (a.items) {  // the work list: this workgroup's slot
+    const int4 m = reinterpret_cast<const int4*>(a.items)[blockIdx.x];
+    if (m.y <= 0) return;  // an empty slot (uniform over the workgroup)
+    attn_item<PRE>(a, smem, m.x, m.y, m.z, m.w & 0xffff, static_cast<int>(static_cast<uint32_t>(m.w) >> 16) * kQ);
+    return;
+  }
+  // Workgroup -> (sequence, head, query block).  Hardware hands workgroup i
+  // to XCD i % 8.  The (sequence, head) pairs, in seq_order's order, go to the
+  // XCDs round-robin, and an XCD's workgroups take its pairs' query blocks in
+  // turn, so the blocks of one pair run on one XCD close together and share
+  // its L2 for the pair's K/V tiles.
+  const int nblk = (a.max_q + kQ - 1) / kQ;
+  const int xcd = blockIdx.x & 7, kx = blockIdx.x >> 3;
+  const int pair = xcd + 8 * (kx / nblk);
+  if (pair >= a.H * a.B) return;  // uniform over the workgroup
+  const int zs = pair / a.H, h = pair - zs * a.H;
+  int qlen, klen;
+  int64_t row0;
+  if (a.seq_meta) {
+    const int4 m = reinterpret_cast<const int4*>(a.seq_meta)[zs];
+    row0 = m.x;
+    qlen = m.y;
+    klen = m.z;
+  } else {
+    const int b = a.seq_order ? a.seq_order[zs] : zs;
+    qlen = a.q_len ? a.q_len[b] : a.uniform_L;
+    // keys never extend past the rows a sequence owns (a caller's k_len > L
+    // in the padded layout is clamped rather than read out of bounds)
+    klen = a.seq_start ? a.k_len[b] : max(0, min(a.k_len[b], a.uniform_L));
+    row0 = a.seq_start ? a.seq_start[b] : static_cast<int64_t>(b) * a.uniform_L;
+  }
+  const int q0 = (kx % nblk) * kQ;
+  if (q0 >= qlen) return;  // uniform over the workgroup
+  attn_item<PRE>(a, smem, row0, qlen, klen, h, q0);
+}
+
+// Work list (launch_attn_items): one thread per slot.  Slot (workgroup) s
+// runs on XCD s % 8 and is place pos = s / 8 of that XCD's list, which holds
+// the items of runs x, x + 8, x + 16, ... (runs of kAttnRun items of the
+// batch's item order).  Item i's sequence z is found by bisection of the
+// table's query-block prefix.
+__global__ __launch_bounds__(256) void attn_items_kernel(const int32_t* table, int Bb, int H, int n_slots,
+                                                         int32_t* items) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  if (s >= n_slots) return;
+  const int32_t* qbp = table + seq_table_qbp(Bb);
+  const int32_t* meta = table + seq_table_meta(Bb);
+  const int pos = s >> 3;
+  const int64_t i = (static_cast<int64_t>(pos / kAttnRun) * 8 + (s & 7)) * kAttnRun + pos % kAttnRun;
+  int4 out = {0, 0, 0, 0};
+  if (i < static_cast<int64_t>(H) * qbp[Bb]) {
+    int lo = 0, hi = Bb;  // H * qbp[lo] <= i < H * qbp[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (static_cast<int64_t>(H) * qbp[mid] <= i)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    const int nb = qbp[lo + 1] - qbp[lo];  // >= 1: item i lies in sequence lo's range
+    const int r = static_cast<int>(i - static_cast<int64_t>(H) * qbp[lo]);
+    const int h = r / nb, qb = r - h * nb;
+    out = (int4){meta[4 * lo], meta[4 * lo + 1], meta[4 * lo + 2], h | (qb << 16)};
+  }
+  reinterpret_cast<int4*>(items)[s] = out;
+}
+
 // ------------------------------------------------------------------ generic
 constexpr int gQ = 128;   // queries per workgroup (one per thread)
 constexpr int gKey = 32;  // keys per LDS tile
@@ -474,9 +519,17 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
                     aligned16(a.v) && (reinterpret_cast<uintptr_t>(a.o) & 7u) == 0;
   if (mfma) {
     // one workgroup per (sequence, head, query block), the pairs padded to a
-    // multiple of the 8 XCDs (see the kernel's mapping)
-    const int64_t pairs8 = (static_cast<int64_t>(a.H) * a.B + 7) / 8 * 8;
-    const int64_t nwg = pairs8 * ((a.max_q + kQ - 1) / kQ);
+    // multiple of the 8 XCDs (see the kernel's mapping), or per slot of the
+    // work list
+    int64_t nwg;
+    if (a.items) {
+      require(a.n_slots > 0 && (reinterpret_cast<uintptr_t>(a.items) & 15u) == 0,
+              "attention: the work list needs slots and 16-byte alignment");
+      nwg = a.n_slots;
+    } else {
+      const int64_t pairs8 = (static_cast<int64_t>(a.H) * a.B + 7) / 8 * 8;
+      nwg = pairs8 * ((a.max_q + kQ - 1) / kQ);
+    }
     require(nwg < (int64_t{1} << 31), "attention: too many workgroups");
     if (a.q_log2_scaled)
       attn_bf16_mfma_kernel<true><<<dim3(static_cast<unsigned>(nwg)), dim3(256), 0, st>>>(a);
@@ -491,6 +544,24 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
   else
     launch_generic<float>(a, st);
   check_launch("attn_generic");
+}
+
+int attn_item_slots(int Tb, int Bb, int H) {
+  require(Tb >= 0 && Bb >= 0 && H > 0, "attention items: bad shape");
+  // sum over sequences of ceil(n / kAttnQ) <= (T + (kAttnQ - 1) B) / kAttnQ
+  const int64_t items = static_cast<int64_t>(H) * ((static_cast<int64_t>(Tb) + (kAttnQ - 1) * int64_t{Bb} + kAttnQ - 1) / kAttnQ);
+  const int64_t slots = 8 * ((items + 8 * kAttnRun - 1) / (8 * kAttnRun)) * kAttnRun;
+  require(slots < (int64_t{1} << 30), "attention items: too many");
+  return static_cast<int>(slots);
+}
+
+void launch_attn_items(const int32_t* table, int Bb, int H, int n_slots, int32_t* items, hipStream_t st) {
+  if (n_slots <= 0) return;
+  require(table && items && (reinterpret_cast<uintptr_t>(items) & 15u) == 0 && Bb >= 1 && H >= 1 &&
+              H < 65536 && n_slots % 8 == 0,
+          "attention items: bad arguments");
+  attn_items_kernel<<<(n_slots + 255) / 256, 256, 0, st>>>(table, Bb, H, n_slots, items);
+  check_launch("attn_items");
 }
 
 }  // namespace sjh

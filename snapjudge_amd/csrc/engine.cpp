@@ -547,13 +547,18 @@ void fill_seq_table(const BatchPlan& p, const int32_t* qtype, int32_t* t) {
     seq_start[4 * Bb + b] = real ? p.order[u] : b;
   }
   int32_t* meta = t + seq_table_meta(Bb);
+  int32_t* qbp = t + seq_table_qbp(Bb);
+  int nqb = 0;
   for (int z = 0; z < Bb; ++z) {
     const int b = seq_start[4 * Bb + z];
     meta[4 * z + 0] = seq_start[b];
     meta[4 * z + 1] = seq_start[Bb + b];
     meta[4 * z + 2] = seq_start[2 * Bb + b];
     meta[4 * z + 3] = 0;
+    qbp[z] = nqb;
+    nqb += (meta[4 * z + 1] + kAttnQ - 1) / kAttnQ;
   }
+  qbp[Bb] = nqb;
 }
 }  // namespace
 
@@ -634,6 +639,8 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   tok_pos_.ensure(t * 4);
   tok_seq_.ensure(t * 4);
   seqinfo_.ensure(seq_table_ints(std::max(nB, 1)) * 4);
+  const int n_items = attn_item_slots(nT, nB, H_);
+  attn_items_.ensure(static_cast<size_t>(n_items) * 16);
   X_.ensure(t * D * 4);
   Y_.ensure(t * D * as);
   QKV_.ensure(t * 3 * D * as);
@@ -657,6 +664,8 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   ws_.Z = Z_.as<float>();
   ws_.partial = splitk_.as<float>();
   ws_.partial_cap = static_cast<int64_t>(splitk_.bytes() / 4);
+  ws_.attn_items = attn_items_.as<int32_t>();
+  ws_.attn_slots_cap = n_items;
   ++ws_gen_;
   for (auto& kv : graphs_)
     if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
@@ -832,6 +841,13 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
   void* G = w.G;
 
   launch_token_index(seq_start, q_len, Bb, w.tok_pos, w.tok_seq, st);
+  // the attention work list of the batch, when the bf16 head_dim-64 kernel runs
+  const bool attn_list = adt == DT_BF16 && Dh_ == 64 && w.attn_items;
+  const int attn_slots = attn_list ? attn_item_slots(T, Bb, H_) : 0;
+  if (attn_list) {
+    require(attn_slots <= w.attn_slots_cap, "attention work list: workspace too small");
+    launch_attn_items(si, Bb, H_, attn_slots, w.attn_items, st);
+  }
 
   // src/model.cpp:332-340: X = LN(emb[ids]); layer 0 reads X itself.  BERT
   // family (src/sj_model.cpp:220-237): X = LN(word[ids] + pos[position] ; w, b)
@@ -960,6 +976,10 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       a.window = ly.window;
       a.scale = scale;
       a.q_log2_scaled = q_pre;
+      if (attn_list) {
+        a.items = w.attn_items;
+        a.n_slots = attn_slots;
+      }
       attn("attention", a, st);
     }
     {  // X += O . Wo^T (src/model.cpp:389-391)
@@ -1340,6 +1360,8 @@ size_t Engine::scratch_layout(const BatchPlan& p, Ws& ws) const {
   const size_t Z = lora_r_ > 0 ? take(t * static_cast<size_t>(lora_r_) * 4) : 0;
   const size_t part_floats = p.Tb <= 256 ? 16 * t * D : 0;
   const size_t part = take(part_floats * 4);
+  const int n_items = attn_item_slots(p.Tb, p.Bb, H_);
+  const size_t items = take(static_cast<size_t>(n_items) * 16);
   ws = Ws();
   if (off > kScratchBytes) return off;
   ws.seq = reinterpret_cast<int32_t*>(scratch_ + seq);
@@ -1352,6 +1374,8 @@ size_t Engine::scratch_layout(const BatchPlan& p, Ws& ws) const {
   ws.Z = lora_r_ > 0 ? reinterpret_cast<float*>(scratch_ + Z) : nullptr;
   ws.partial = part_floats ? reinterpret_cast<float*>(scratch_ + part) : nullptr;
   ws.partial_cap = static_cast<int64_t>(part_floats);
+  ws.attn_items = reinterpret_cast<int32_t*>(scratch_ + items);
+  ws.attn_slots_cap = n_items;
   return off;
 }
 

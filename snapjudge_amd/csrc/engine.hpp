@@ -97,6 +97,8 @@ struct Ws {
   float* Z = nullptr;  // LoRA [Tb, r]
   float* partial = nullptr;  // split-K partial sums
   int64_t partial_cap = 0;   // floats
+  int32_t* attn_items = nullptr;  // attention work list (AttnArgs::items)
+  int attn_slots_cap = 0;         // its slots
 };
 
 class Engine {
@@ -235,6 +237,7 @@ class Engine {
   DevBuf X2_, expand_idx_;  // forward_shared: hidden states of the (sequence, qtype) pairs
   std::vector<int32_t> tail_hidx_;  // host copy of the head tail's row indices
   DevBuf splitk_;  // split-K partial sums for short batches (GemmArgs::partial)
+  DevBuf attn_items_;  // attention work list (AttnArgs::items)
   Ws ws_;          // views of the buffers above
   DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_lg_, tail_ain_, tail_ah_,
       tail_ao_, tail_act_;

@@ -540,7 +540,6 @@ __global__ __launch_bounds__(kSeqTableMaxB) void seq_table_kernel(SeqTableArgs a
     t[2] = 0;
     t[3] = 0;
   }
-  if (b >= a.Bb) return;
   int rank = b;  // empty entries keep their place after the real sequences
   if (b < a.B) {
     rank = 0;
@@ -549,6 +548,26 @@ __global__ __launch_bounds__(kSeqTableMaxB) void seq_table_kernel(SeqTableArgs a
       rank += (m > n || (m == n && c < b)) ? 1 : 0;
     }
   }
+  // attention query blocks per entry, in table order, and their prefix
+  // (ranks are a permutation of [0, Bb); entries past Bb have none)
+  __syncthreads();  // every thread is done with start_s
+  start_s[b] = 0;
+  __syncthreads();
+  if (b < a.Bb) start_s[rank] = (n + kAttnQ - 1) / kAttnQ;
+  __syncthreads();
+  int qb_incl = start_s[b];
+  const int qb_own = qb_incl;
+  for (int off = 1; off < kSeqTableMaxB; off <<= 1) {
+    const int add = b >= off ? start_s[b - off] : 0;
+    __syncthreads();
+    qb_incl += add;
+    start_s[b] = qb_incl;
+    __syncthreads();
+  }
+  int32_t* qbp = t + seq_table_qbp(a.Bb);
+  if (b == 0) qbp[a.Bb] = start_s[kSeqTableMaxB - 1];  // the total
+  if (b >= a.Bb) return;
+  qbp[b] = qb_incl - qb_own;  // exclusive prefix
   int32_t* seq_start = t + kSeqHdr;
   seq_start[b] = start;
   seq_start[a.Bb + b] = n;       // q_len

@@ -149,8 +149,30 @@ struct AttnArgs {
   // projection): the logits come out of the QK^T product in the log2 domain.
   // bf16 with head_dim 64 only.
   bool q_log2_scaled = false;
+  // Optional work list of the bf16 head_dim-64 kernel (launch_attn_items),
+  // 16-byte aligned: n_slots entries of {first row, q_len, k_len, head |
+  // query block << 16}, q_len 0 for an empty slot; workgroup w runs slot w.
+  // The grid is then n_slots workgroups whatever B and max_q say.
+  const int* items = nullptr;
+  int n_slots = 0;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);
+
+// Attention work list of a batch (AttnArgs::items): the (sequence, head,
+// query block of kAttnQ rows) items of the sequences in table order (longest
+// first), each sequence's heads in turn and each head's blocks in turn, are
+// cut into runs of kAttnRun consecutive items dealt to the 8 XCDs
+// round-robin; the workgroups of an XCD take its runs' items in order.
+// Items beyond the batch's leave their slots empty.  Only real items reach
+// the dispatcher (the padded grid of the (pair, block) mapping hands it an
+// empty workgroup for every block a shorter sequence lacks).
+constexpr int kAttnQ = 128;
+constexpr int kAttnRun = 4;
+// Slots for any batch of at most Tb rows in at most Bb sequences (a multiple
+// of 8 * kAttnRun).
+int attn_item_slots(int Tb, int Bb, int H);
+// Fills items[0, n_slots) from the sequence table (its query-block prefix).
+void launch_attn_items(const int32_t* table, int Bb, int H, int n_slots, int32_t* items, hipStream_t st);
 
 // Standalone RoPE on packed (q|k|v)(head)(dim) rows, position = pos[r]
 // (or r % L when pos is null), as src/tensor.cpp:257-279.
@@ -182,13 +204,16 @@ void launch_quantize_fp8_rows(const float* w, int64_t rows, int64_t cols, uint8_
 //   [0] total tokens T = sum of lens, [1] B, [2..3] 0,
 //   seq_start[Bb] at 4, q_len[Bb], k_len[Bb], qtype[Bb], order[Bb], then,
 //   16-byte aligned at seq_table_meta(Bb), meta[4 * Bb] = {seq_start, q_len,
-//   k_len, 0} of order[z] for z < Bb.
+//   k_len, 0} of order[z] for z < Bb, then at seq_table_qbp(Bb) the query
+//   block prefix qbp[Bb + 1]: qbp[z] = sum over z' < z of
+//   ceil(q_len / kAttnQ) of order[z'].
 // Entries b >= B are empty sequences (start T, length 0) that every kernel
 // skips; order lists the real sequences longest first (stable), then the
 // empty ones.
 constexpr int kSeqHdr = 4;
-inline size_t seq_table_meta(int Bb) { return (static_cast<size_t>(kSeqHdr) + 5u * Bb + 3) / 4 * 4; }
-inline size_t seq_table_ints(int Bb) { return seq_table_meta(Bb) + 4u * Bb; }
+__host__ __device__ inline size_t seq_table_meta(int Bb) { return (static_cast<size_t>(kSeqHdr) + 5u * Bb + 3) / 4 * 4; }
+__host__ __device__ inline size_t seq_table_qbp(int Bb) { return seq_table_meta(Bb) + 4u * Bb; }
+__host__ __device__ inline size_t seq_table_ints(int Bb) { return (seq_table_qbp(Bb) + Bb + 1 + 3) / 4 * 4; }
 // Builds that table on the device from lengths passed by value in the kernel
 // arguments (no host staging buffer): q_len = k_len = lens[b], qtype 0.
 constexpr int kSeqTableMaxB = 256;
