@@ -37,7 +37,7 @@ __device__ __forceinline__ void tile_epilogue(const float* Cs, int ldcs, int m0,
       const int m = m0 + r, j = j0 + c;
       if (m < g.M && j < g.N) {
         const float in = Cs[r * ldcs + c], gate = Cs[r * ldcs + HB + c];
-        store_f32(out + static_cast<int64_t>(m) * g.ldo + j, gelu_erf(in) * gate);
+        store_f32(out + static_cast<int64_t>(m) * g.ldo + j, gelu_out<OutT>(in) * gate);
       }
     }
     return;
@@ -73,7 +73,7 @@ __device__ __forceinline__ void tile_epilogue(const float* Cs, int ldcs, int m0,
     } else {
       if (g.bias) v += g.bias[n];
       if (g.act == 1)
-        v = gelu_erf(v);
+        v = gelu_out<OutT>(v);
       else if (g.act == 2)
         v = fmaxf(v, 0.f);
     }
@@ -175,7 +175,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
 #pragma unroll
         for (int j = 0; j < TJ / 2; ++j) {
           const int col = c0 + j * 32;
-          if (col < g.N) store_f32(orow + col, gelu_erf(acc[i][j][e]) * acc[i][j + TJ / 2][e]);
+          if (col < g.N) store_f32(orow + col, gelu_out<OutT>(acc[i][j][e]) * acc[i][j + TJ / 2][e]);
         }
       }
   } else if constexpr (EPI == EPI_RESID) {
@@ -330,7 +330,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
           if (col >= g.N) continue;
           float v = acc[i][j][e] + bv[j];
           if (g.act == 1)
-            v = gelu_erf(v);
+            v = gelu_out<OutT>(v);
           else if (g.act == 2)
             v = fmaxf(v, 0.f);
           store_f32(orow + col, v);
@@ -559,7 +559,7 @@ __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            v[r] = gelu_erf(acc[i][j][4 * q + r]) * acc[i][j + TJ / 2][4 * q + r];
+            v[r] = gelu_out<OutT>(acc[i][j][4 * q + r]) * acc[i][j + TJ / 2][4 * q + r];
           store4(orow + j * 32 + 8 * q, v[0], v[1], v[2], v[3]);
         }
     }
@@ -664,7 +664,7 @@ __device__ __forceinline__ void pers_epilogue(const GemmArgs& g, f32x16_t (&acc)
           for (int t = 0; t < 4; ++t) {
             v[t] = acc[i][j][4 * q + t] + b[t];
             if (g.act == 1)
-              v[t] = gelu_erf(v[t]);
+              v[t] = gelu_out<OutT>(v[t]);
             else if (g.act == 2)
               v[t] = fmaxf(v[t], 0.f);
           }
@@ -1243,7 +1243,7 @@ __device__ void splitk_output(const GemmArgs& g, int S, int m, int n) {
   }
   OutT* out = static_cast<OutT*>(g.out) + static_cast<int64_t>(m) * g.ldo + n;
   if (g.epi == EPI_GEGLU) {
-    store_f32(out, gelu_erf(splitk_sum(g, S, m, n)) * splitk_sum(g, S, m, g.N + n));
+    store_f32(out, gelu_out<OutT>(splitk_sum(g, S, m, n)) * splitk_sum(g, S, m, g.N + n));
     return;
   }
   float v = splitk_sum(g, S, m, n);
@@ -1263,7 +1263,7 @@ __device__ void splitk_output(const GemmArgs& g, int S, int m, int n) {
   } else {
     if (g.bias) v += g.bias[n];
     if (g.act == 1)
-      v = gelu_erf(v);
+      v = gelu_out<OutT>(v);
     else if (g.act == 2)
       v = fmaxf(v, 0.f);
   }

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 namespace sjh {
@@ -51,6 +52,31 @@ __device__ __forceinline__ bf16x8_t fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
 // Exact erf GELU, the reference's activation (src/tensor.cpp:96-98).
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654757f));
+}
+
+// GELU for outputs rounded to bf16, with the erf of Abramowitz & Stegun
+// 7.1.26 (|erf error| <= 1.5e-7): 1 + erf(z) = 2 - q for z >= 0 and q for
+// z < 0, q = erfc(|z|) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
+// t = 1 / (1 + p |z|).  No branches (erff branches per element) and no
+// cancellation for negative inputs; within 4.3e-7 of the exact GELU.
+__device__ __forceinline__ float gelu_as(float x) {
+  constexpr float kP = 0.3275911f, kA1 = 0.254829592f, kA2 = -0.284496736f, kA3 = 1.421413741f,
+                  kA4 = -1.453152027f, kA5 = 1.061405429f;
+  const float z = fabsf(x) * 0.70710678118654757f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(kP, z, 1.f));
+  const float poly = t * __builtin_fmaf(t, __builtin_fmaf(t, __builtin_fmaf(t, __builtin_fmaf(t, kA5, kA4), kA3), kA2), kA1);
+  const float q = poly * __builtin_amdgcn_exp2f(-1.4426950408889634f * z * z);
+  return 0.5f * x * (x >= 0.f ? 2.f - q : q);
+}
+
+// GELU of a GEMM epilogue: the branch-free form where the output is rounded
+// to bf16, erff (the reference's function) for fp32 outputs.
+template <typename OutT>
+__device__ __forceinline__ float gelu_out(float x) {
+  if constexpr (std::is_same<OutT, bf16_t>::value)
+    return gelu_as(x);
+  else
+    return gelu_erf(x);
 }
 
 // Rotate-half RoPE on one pair (x0 = dim d, x1 = dim d + Dh/2), as
