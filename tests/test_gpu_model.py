@@ -199,6 +199,32 @@ def test_cfg3_shape_sampled_rows_and_batch_invariance(orc):
     m.close()
 
 
+def test_more_than_256_sequences(orc):
+    # More than 256 sequences: the sequence table, with the query-block prefix
+    # that the attention work list is cut from, is filled on the host instead
+    # of by the device kernel.  Sampled rows (one and two 128-query blocks,
+    # both ends of the length order) against the oracle on each row alone;
+    # reversing the batch permutes the outputs bit for bit.
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg2"], num_hidden_layers=2), seed=51)
+    cfg = synth.flat_cfg(rl, enc)
+    lens = np.random.default_rng(52).integers(1, 201, size=300)
+    ids, mask, lens = synth.batch_with_lens(lens, int(lens.max()), cfg["vocab_size"], seed=53)
+    m = sj.Model(w, cfg, precision=BF16)
+    h = m.encode(ids, mask)
+    om = orc.model(w, cfg)
+    order = np.argsort(lens, kind="stable")
+    for b in (order[0], order[150], order[-1], 0, 256, 299):
+        n = int(lens[b])
+        ref = om.encode(ids[b:b + 1, :n], mask[b:b + 1, :n])[0]
+        err = float(np.abs(h[b, :n] - ref).max())
+        print(f"B=300 row {b} n={n} max|d|={err:.3g}", flush=True)
+        assert err <= TOL[BF16]
+    hr = m.encode(ids[::-1].copy(), mask[::-1].copy())
+    assert np.array_equal(hr[::-1], h)
+    assert np.all(h[~mask.astype(bool)] == 0)
+    m.close()
+
+
 @pytest.fixture(scope="module")
 def cfg4(golden_dir):
     g = np.load(os.path.join(golden_dir, "cfg4_b4s8192.npz"))
