@@ -1187,7 +1187,9 @@ void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
 #endif
 // fp8 weights: 48 KB stages (bf16 A rows, fp8 W rows), three in the ring; 8 waves
 // of 128 x 64 (one workgroup per CU, 256 VGPRs per wave)
+#ifndef SJH_GEMM_PERS_FP8
 #define SJH_GEMM_PERS_FP8 256, 256, 2, 4, 3, 64
+#endif
 
 #ifndef SJH_GEMM_SMALL
 #define SJH_GEMM_SMALL 64, 64, 2, 1, 4, 64
