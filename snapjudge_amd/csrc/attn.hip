@@ -560,6 +560,8 @@ void launch_attn_items(const int32_t* table, int Bb, int H, int n_slots, int32_t
   require(table && items && (reinterpret_cast<uintptr_t>(items) & 15u) == 0 && Bb >= 1 && H >= 1 &&
               H < 65536 && n_slots % 8 == 0,
           "attention items: bad arguments");
+  // (the caller keeps every sequence below 65536 query blocks: the item
+  // holds the block index in 16 bits)
   attn_items_kernel<<<(n_slots + 255) / 256, 256, 0, st>>>(table, Bb, H, n_slots, items);
   check_launch("attn_items");
 }

@@ -842,7 +842,8 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
 
   launch_token_index(seq_start, q_len, Bb, w.tok_pos, w.tok_seq, st);
   // the attention work list of the batch, when the bf16 head_dim-64 kernel runs
-  const bool attn_list = adt == DT_BF16 && Dh_ == 64 && w.attn_items;
+  // (the list holds a query block's index in 16 bits)
+  const bool attn_list = adt == DT_BF16 && Dh_ == 64 && w.attn_items && p.max_qb <= 65536 * kAttnQ;
   const int attn_slots = attn_list ? attn_item_slots(T, Bb, H_) : 0;
   if (attn_list) {
     require(attn_slots <= w.attn_slots_cap, "attention work list: workspace too small");
