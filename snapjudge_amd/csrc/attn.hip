@@ -150,15 +150,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     }
   };
 
+  // O^T accumulators; l_i: this lane's share of the softmax denominator,
+  // summed from the same bf16 weights the P.V MFMA consumes (two partial
+  // sums, v_dot2 with ones); m_i: the running offset.  Each pass sets them.
   f32x16_t o[2];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    o[0][e] = 0.f;
-    o[1][e] = 0.f;
-  }
-  // l_i: this lane's share of the softmax denominator, summed from the same
-  // bf16 weights the P.V MFMA consumes (two partial sums, v_dot2 with ones)
-  float m_i = -INFINITY, l_i = 0.f, l_j = 0.f;
+  float m_i, l_i, l_j;
   const float c = PRE ? 1.f : a.scale * kLog2e;
 
   // LDS offsets (within a stage) of this lane's operand reads, the same for
@@ -184,9 +180,12 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
 
   // One 64-key tile at key offset kt from the stage at sb.  MASK 0: interior
   // tile of full attention; 1: its last tile (keys >= qhi masked); 2: a
-  // sliding window (keys outside [qlo, qhi) masked).
-  auto tile = [&](auto mask_tag, const char* sb, int kt) {
+  // sliding window (keys outside [qlo, qhi) masked).  NOMAX (PRE only): the
+  // exp2 offset stays 0 and no tile max is taken (see the pass check below).
+  auto tile = [&](auto mask_tag, auto nomax_tag, const char* sb, int kt) {
     constexpr int MASK = decltype(mask_tag)::value;
+    constexpr bool NOMAX = decltype(nomax_tag)::value;
+    static_assert(PRE || !NOMAX, "the offset-free pass needs log2-domain logits");
     // S^T[key][query] for keys kt + [0, 32) and kt + [32, 64)
     f32x16_t s[2];
 #pragma unroll
@@ -217,32 +216,34 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     // normalisation uses the same m_i, so the result is exact while the
     // rescale of O and l is skipped for most tiles.  PRE: the same with the
     // offset held at 0 while the logits stay near 0 (kZeroLo, kZeroHi).
-    float tmax = -INFINITY;
+    if constexpr (!NOMAX) {
+      float tmax = -INFINITY;
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
+      for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[jb][e]);
-    tmax = wave_max32(tmax) * c;
-    const bool bump = tmax > m_i + (PRE ? kLazyPre : kLazy);
-    if (__any(bump)) {
-      asm volatile("" ::: "memory");  // keep this a branch (rarely taken), not a select
-      const float m_tgt = PRE && tmax >= kZeroLo && tmax <= kZeroHi ? 0.f : tmax;
-      const float m_new = bump ? m_tgt : m_i;
-      const float alpha = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_new);
-      m_i = m_new;
-      l_i *= alpha;
-      l_j *= alpha;
+        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[jb][e]);
+      tmax = wave_max32(tmax) * c;
+      const bool bump = tmax > m_i + (PRE ? kLazyPre : kLazy);
+      if (__any(bump)) {
+        asm volatile("" ::: "memory");  // keep this a branch (rarely taken), not a select
+        const float m_tgt = PRE && tmax >= kZeroLo && tmax <= kZeroHi ? 0.f : tmax;
+        const float m_new = bump ? m_tgt : m_i;
+        const float alpha = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_new);
+        m_i = m_new;
+        l_i *= alpha;
+        l_j *= alpha;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        o[0][e] *= alpha;
-        o[1][e] *= alpha;
+        for (int e = 0; e < 16; ++e) {
+          o[0][e] *= alpha;
+          o[1][e] *= alpha;
+        }
       }
     }
     const float m_use = m_i == -INFINITY ? 0.f : m_i;
     if constexpr (PRE) {
       // the logits are already in the log2 domain; the offset is 0 for the
       // whole wave unless a lane's logits left [kZeroLo, kZeroHi]
-      if (__any(m_use != 0.f)) {
+      if (!NOMAX && __any(m_use != 0.f)) {
         asm volatile("" ::: "memory");  // a branch (rarely taken), not a select
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb)
@@ -286,32 +287,60 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
       }
   };
 
-#pragma unroll
-  for (int st = 0; st < kNS - 1; ++st)
-    if (st < ntiles) issue(st, st);
-
-  auto step = [&](int t, auto mask_tag) {
+  auto step = [&](int t, auto mask_tag, auto nomax_tag) {
     if (t + kNS - 2 < ntiles)
       wait_vmcnt<4 * (kNS - 2)>();
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
     if (t + kNS - 1 < ntiles) issue(t + kNS - 1, (t + kNS - 1) % kNS);
-    if (wave_active) tile(mask_tag, smem + (t % kNS) * kStage, klo + t * kKey);
+    if (wave_active) tile(mask_tag, nomax_tag, smem + (t % kNS) * kStage, klo + t * kKey);
   };
-  // The interior tiles of full attention run in a loop of their own, then the
-  // masked ones: no branch between the two tile bodies inside the hot loop
-  // (such a merge costs register copies of the accumulators on every tile).
+  // One pass over the item's key tiles.  The interior tiles of full attention
+  // run in a loop of their own, then the masked ones: no branch between the
+  // two tile bodies inside the hot loop (such a merge costs register copies
+  // of the accumulators on every tile).
   const int n_plain = a.window > 0 ? 0 : (khi - klo) / kKey;
-  int t = 0;
-  for (; t < n_plain; ++t) step(t, std::integral_constant<int, 0>{});
-  if (a.window > 0)
-    for (; t < ntiles; ++t) step(t, std::integral_constant<int, 2>{});
-  else
-    for (; t < ntiles; ++t) step(t, std::integral_constant<int, 1>{});
-
-  l_i += l_j;
-  const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
+  auto pass = [&](auto nomax_tag) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      o[0][e] = 0.f;
+      o[1][e] = 0.f;
+    }
+    m_i = -INFINITY, l_i = 0.f, l_j = 0.f;
+#pragma unroll
+    for (int st = 0; st < kNS - 1; ++st)
+      if (st < ntiles) issue(st, st);
+    int t = 0;
+    for (; t < n_plain; ++t) step(t, std::integral_constant<int, 0>{}, nomax_tag);
+    if (a.window > 0)
+      for (; t < ntiles; ++t) step(t, std::integral_constant<int, 2>{}, nomax_tag);
+    else
+      for (; t < ntiles; ++t) step(t, std::integral_constant<int, 1>{}, nomax_tag);
+    l_i += l_j;
+    return l_i + __shfl_xor(l_i, 32, 64);
+  };
+  float l_tot;
+  if constexpr (PRE) {
+    // First pass without the running max: p = 2^s straight from the MFMA.
+    // It stands when every live query's weight sum lies in [2^-60, 2^64]:
+    // then no weight, sum or O entry overflowed, and a weight that flushed
+    // to zero (below 2^-126) is under 2^-53 of the largest one (>= 2^-60 /
+    // 8192), so its loss is far below the bf16 rounding of the weights.
+    // Otherwise (or a NaN) the workgroup runs the item again with the max
+    // rule.  The decision is per workgroup: its waves share the K/V loads.
+    int* redo = reinterpret_cast<int*>(smem + kNS * kStage);
+    if (tid == 0) *redo = 0;  // ordered before other waves' writes by pass 1's barriers
+    l_tot = pass(std::true_type{});
+    if (ntiles > 0) {  // uniform
+      const bool bad = wave_active && qi < qlen && qhi > qlo && !(l_tot >= 0x1p-60f && l_tot <= 0x1p64f);
+      if (__any(bad) && lane == 0) *redo = 1;
+      __syncthreads();
+      if (*redo) l_tot = pass(std::false_type{});
+    }
+  } else {
+    l_tot = pass(std::false_type{});
+  }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qi < qlen) {
     bf16_t* O = static_cast<bf16_t*>(a.o) + (row0 + qi) * a.ld_o + h * 64;
@@ -330,7 +359,8 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
 
 template <bool PRE>
 __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kNS * kStage];
+  // the K/V ring, then the workgroup's redo flag
+  __shared__ __attribute__((aligned(16))) char smem[kNS * kStage + 16];
   if (a.items) {  // the work list: this workgroup's slot
     const int4 m = reinterpret_cast<const int4*>(a.items)[blockIdx.x];
     if (m.y <= 0) return;  // an empty slot (uniform over the workgroup)

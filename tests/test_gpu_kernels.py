@@ -201,12 +201,16 @@ def test_attention_reference_layout(orc, dtype, Dh, window):
     assert float(np.abs(got - want).max()) <= tol
 
 
-@pytest.mark.parametrize("case", ["plain", "window", "large", "negative", "long"])
+@pytest.mark.parametrize("case", ["plain", "window", "large", "negative", "long", "moderate", "mixed"])
 def test_attention_log2_scaled_queries(orc, case):
     # the encoder's layout: q pre-multiplied by scale * log2(e) before its bf16
-    # rounding.  "large" logits (std 20) raise the softmax offset above zero,
-    # "negative" ones (all below -64 in log2 units) start it below; "long"
-    # rows cross many key tiles
+    # rounding.  The kernel first runs an item without a softmax offset and
+    # keeps it when every weight sum lies in [2^-60, 2^64], else runs it again
+    # with the max rule.  "large" logits (std ~29 in log2 units) overflow that
+    # range and take the second pass; "negative" ones (all below -64) fall
+    # under it; "moderate" ones (up to ~45) stay in it; "mixed" has a few
+    # all-negative query rows in each workgroup, which sends the whole
+    # workgroup to the second pass; "long" rows cross many key tiles
     print(f"attn log2 {case}", flush=True)
     B, L, H, Dh = 3, 1100 if case == "long" else 150, 2, 64
     lens = [L, 71, 1] if case != "long" else [L, 700, 64]
@@ -214,8 +218,13 @@ def test_attention_log2_scaled_queries(orc, case):
     qkv = rnd(rng, (B, L, 3, H, Dh))
     if case == "large":
         qkv[:, :, 0] *= 20.0
+    if case == "moderate":
+        qkv[:, :, 0] *= 12.0
     if case == "negative":
         qkv[:, :, 0, :, -1] = -40.0
+        qkv[:, :, 1, :, -1] = 10.0
+    if case == "mixed":
+        qkv[:, :40, 0, :, -1] = -40.0
         qkv[:, :, 1, :, -1] = 10.0
     window = 40 if case == "window" else 0
     c = (1.0 / math.sqrt(Dh)) * math.log2(math.e)
