@@ -67,6 +67,21 @@ __device__ __forceinline__ int kv_off(int row, int col) {
   return row * 128 + (((col >> 3) ^ kv_swz(row)) << 4) + ((col & 7) << 1);
 }
 
+// Buffer descriptor over the memory from p on (untyped dword loads: word 3
+// carries gfx9's 32-bit data format; the record count is the largest, so
+// the range check never clips a load).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const bf16_t* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(p), static_cast<short>(0), 0x7fffffff,
+                                           0x00020000);
+}
+
+// 16 bytes per lane from buffer r at voff + soff into LDS at lds + 16 * lane
+// (buffer_load_dwordx4 ... lds; the LDS base goes through M0).
+__device__ __forceinline__ void load_lds16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, char* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16,
+                                           static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+}
+
 // Transposed 8-byte LDS read (ds_read_b64_tr_b16).  Within each 16-lane
 // group, if lane q + 4k addresses element (r0 + k, c0 + 4q) of a row-major
 // tile, lane i of the group receives elements (r0 + k, c0 + i), k = 0..3.
@@ -113,9 +128,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
   // wave w moves groups w, w + 4, w + 8, w + 12.  Lane l carries row
   // 8 * (group % 8) + l / 8 and lands in chunk slot l % 8, so it reads the
   // logical chunk (l % 8) ^ kv_swz(row).
-  // Groups i = 0, 1 are K rows, 2, 3 V rows.  A full tile adds the lane's
-  // fixed byte offset to a wave-uniform row base; only a tile that runs past
-  // klen clamps its rows one by one.
+  // Groups i = 0, 1 are K rows, 2, 3 V rows.  The loads go through buffer
+  // descriptors based at the sequence's first K and V rows: a full tile is
+  // the tile's row offset (scalar) plus the lane's fixed byte offset, with no
+  // per-lane address arithmetic; only a tile that runs past klen clamps its
+  // rows one by one (32-bit lane offsets from the sequence's base).
   const int lrow = lane >> 3, cslot = lane & 7;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   uint32_t goff[4];
@@ -124,28 +141,26 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     const int r = 8 * ((wave + 4 * i) & 7) + lrow;
     goff[i] = static_cast<uint32_t>(r * (i < 2 ? a.ld_k : a.ld_v) * 2 + ((cslot ^ kv_swz(r)) << 4));
   }
+  const __amdgpu_buffer_rsrc_t rk = seq_rsrc(K + row0 * a.ld_k);
+  const __amdgpu_buffer_rsrc_t rv = seq_rsrc(V + row0 * a.ld_v);
+  const uint32_t kstride = static_cast<uint32_t>(a.ld_k * 2), vstride = static_cast<uint32_t>(a.ld_v * 2);
   auto issue = [&](int t, int buf) {
     char* base = smem + buf * kStage;
     const int k0 = klo + t * kKey;
     if (k0 + kKey <= klen) {
-      const char* kb = reinterpret_cast<const char*>(K + (row0 + k0) * a.ld_k);
-      const char* vb = reinterpret_cast<const char*>(V + (row0 + k0) * a.ld_v);
+      const uint32_t sk = static_cast<uint32_t>(k0) * kstride, sv = static_cast<uint32_t>(k0) * vstride;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        load_lds16((i < 2 ? kb : vb) + goff[i], base + (wave_s + 4 * i) * 1024);
+        load_lds16_buf(i < 2 ? rk : rv, goff[i], i < 2 ? sk : sv, base + (wave_s + 4 * i) * 1024);
     } else {
-      // rows clamped to the last key: the sequence's uniform base plus a
-      // 32-bit per-lane byte offset
-      const char* kq = reinterpret_cast<const char*>(K + row0 * a.ld_k);
-      const char* vq = reinterpret_cast<const char*>(V + row0 * a.ld_v);
+      // rows clamped to the last key
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int grp = wave_s + 4 * i;
         const int r = 8 * (grp & 7) + lrow;
         const uint32_t key = static_cast<uint32_t>(min(k0 + r, klen - 1));
-        const uint32_t off = key * static_cast<uint32_t>((i < 2 ? a.ld_k : a.ld_v) * 2) +
-                             ((cslot ^ kv_swz(r)) << 4);
-        load_lds16((i < 2 ? kq : vq) + off, base + grp * 1024);
+        const uint32_t off = key * (i < 2 ? kstride : vstride) + ((cslot ^ kv_swz(r)) << 4);
+        load_lds16_buf(i < 2 ? rk : rv, off, 0u, base + grp * 1024);
       }
     }
   };
