@@ -302,14 +302,19 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
       }
   };
 
-  auto step = [&](int t, auto mask_tag, auto nomax_tag) {
+  // ST: the ring slot of tile t when the caller knows it (t % kNS), so the
+  // slot's LDS offset folds into the instructions' offset fields; -1: taken
+  // from t
+  auto step = [&](int t, auto mask_tag, auto nomax_tag, auto slot_tag) {
+    constexpr int ST = decltype(slot_tag)::value;
+    const int slot = ST >= 0 ? ST : t % kNS;
     if (t + kNS - 2 < ntiles)
       wait_vmcnt<4 * (kNS - 2)>();
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
-    if (t + kNS - 1 < ntiles) issue(t + kNS - 1, (t + kNS - 1) % kNS);
-    if (wave_active) tile(mask_tag, nomax_tag, smem + (t % kNS) * kStage, klo + t * kKey);
+    if (t + kNS - 1 < ntiles) issue(t + kNS - 1, ST >= 0 ? (ST + kNS - 1) % kNS : (t + kNS - 1) % kNS);
+    if (wave_active) tile(mask_tag, nomax_tag, smem + slot * kStage, klo + t * kKey);
   };
   // One pass over the item's key tiles.  The interior tiles of full attention
   // run in a loop of their own, then the masked ones: no branch between the
@@ -326,12 +331,19 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
 #pragma unroll
     for (int st = 0; st < kNS - 1; ++st)
       if (st < ntiles) issue(st, st);
+    using I0 = std::integral_constant<int, 0>;
+    using Idyn = std::integral_constant<int, -1>;
+    static_assert(kNS == 2, "the interior loop is unrolled by the ring depth");
     int t = 0;
-    for (; t < n_plain; ++t) step(t, std::integral_constant<int, 0>{}, nomax_tag);
+    for (; t + 1 < n_plain; t += 2) {  // t is even: slots 0 then 1
+      step(t, I0{}, nomax_tag, I0{});
+      step(t + 1, I0{}, nomax_tag, std::integral_constant<int, 1>{});
+    }
+    for (; t < n_plain; ++t) step(t, I0{}, nomax_tag, Idyn{});
     if (a.window > 0)
-      for (; t < ntiles; ++t) step(t, std::integral_constant<int, 2>{}, nomax_tag);
+      for (; t < ntiles; ++t) step(t, std::integral_constant<int, 2>{}, nomax_tag, Idyn{});
     else
-      for (; t < ntiles; ++t) step(t, std::integral_constant<int, 1>{}, nomax_tag);
+      for (; t < ntiles; ++t) step(t, std::integral_constant<int, 1>{}, nomax_tag, Idyn{});
     l_i += l_j;
     return l_i + __shfl_xor(l_i, 32, 64);
   };
