@@ -67,12 +67,12 @@ __device__ __forceinline__ int kv_off(int row, int col) {
   return row * 128 + (((col >> 3) ^ kv_swz(row)) << 4) + ((col & 7) << 1);
 }
 
-// Buffer descriptor over the memory from p on (untyped dword loads: word 3
-// carries gfx9's 32-bit data format; the record count is the largest, so
-// the range check never clips a load).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const bf16_t* p) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(p), static_cast<short>(0), 0x7fffffff,
-                                           0x00020000);
+// Buffer descriptor over the n_bytes bytes from p on (untyped dword loads:
+// word 3 carries gfx9's 32-bit data format).  A load at or past n_bytes
+// returns zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const bf16_t* p, uint32_t n_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(p), static_cast<short>(0),
+                                           static_cast<int>(n_bytes), 0x00020000);
 }
 
 // 16 bytes per lane from buffer r at voff + soff into LDS at lds + 16 * lane
@@ -141,9 +141,12 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     const int r = 8 * ((wave + 4 * i) & 7) + lrow;
     goff[i] = static_cast<uint32_t>(r * (i < 2 ? a.ld_k : a.ld_v) * 2 + ((cslot ^ kv_swz(r)) << 4));
   }
-  const __amdgpu_buffer_rsrc_t rk = seq_rsrc(K + row0 * a.ld_k);
-  const __amdgpu_buffer_rsrc_t rv = seq_rsrc(V + row0 * a.ld_v);
+  // the descriptors end with the head's 64 values of key klen - 1: the rows
+  // past the keys read as zeros
   const uint32_t kstride = static_cast<uint32_t>(a.ld_k * 2), vstride = static_cast<uint32_t>(a.ld_v * 2);
+  const uint32_t klast = static_cast<uint32_t>(max(klen - 1, 0));
+  const __amdgpu_buffer_rsrc_t rk = seq_rsrc(K + row0 * a.ld_k, klast * kstride + 128u);
+  const __amdgpu_buffer_rsrc_t rv = seq_rsrc(V + row0 * a.ld_v, klast * vstride + 128u);
   auto issue = [&](int t, int buf) {
     char* base = smem + buf * kStage;
     const int k0 = klo + t * kKey;
@@ -153,12 +156,13 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
       for (int i = 0; i < 4; ++i)
         load_lds16_buf(i < 2 ? rk : rv, goff[i], i < 2 ? sk : sv, base + (wave_s + 4 * i) * 1024);
     } else {
-      // rows clamped to the last key
+      // the tile that runs past the keys: its rows past klen - 1 lie outside
+      // the descriptors' range and land as zeros
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int grp = wave_s + 4 * i;
         const int r = 8 * (grp & 7) + lrow;
-        const uint32_t key = static_cast<uint32_t>(min(k0 + r, klen - 1));
+        const uint32_t key = static_cast<uint32_t>(k0 + r);
         const uint32_t off = key * (i < 2 ? kstride : vstride) + ((cslot ^ kv_swz(r)) << 4);
         load_lds16_buf(i < 2 ? rk : rv, off, 0u, base + grp * 1024);
       }
@@ -213,7 +217,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
         s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[jb], 0, 0, 0);
       }
     }
-    if constexpr (MASK != 0) {
+    // The last tile of full attention in the offset-free pass needs no mask:
+    // its keys past klen have zero K and V rows, so each adds 2^0 = 1 to the
+    // lane's weight sum and nothing to O; the sum gives them back below.
+    constexpr bool kZeroRows = NOMAX && MASK == 1;
+    if constexpr (MASK != 0 && !kZeroRows) {
       // key of element (jb, e) is kt + 4*hb + 32*jb + 8*(e/4) + e%4
       const int lo = qlo - kt - 4 * hb, hi = qhi - kt - 4 * hb;
 #pragma unroll
@@ -300,6 +308,14 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
         }
       }
+    if constexpr (kZeroRows) {
+      // this lane's keys are kt + 8g + 4hb + [0, 4), g = 0..7; with rr =
+      // klen - kt - 4hb, those at or past klen are all of groups g > rr / 8
+      // and 4 - rr % 8 (if positive) of group rr / 8
+      const int rr = klen - kt - 4 * hb;
+      const int n_out = rr <= 0 ? 32 : rr >= 60 ? 0 : 4 * (7 - (rr >> 3)) + max(0, 4 - (rr & 7));
+      l_i -= static_cast<float>(n_out);
+    }
   };
 
   // ST: the ring slot of tile t when the caller knows it (t % kNS), so the
