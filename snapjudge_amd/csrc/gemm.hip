@@ -154,6 +154,14 @@ __device__ __forceinline__ GemmArgs resolve_rows(const GemmArgs& g0) {
   return g;
 }
 
+// The value lane l ^ 16 holds (v_permlane16_swap of v with itself hands
+// rows 0 and 2 of 16 lanes to rows 1 and 3 in its first result and rows 1
+// and 3 to rows 0 and 2 in its second).  hi_row: lane & 16.
+__device__ __forceinline__ float swap16(float v, bool hi_row) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(hi_row ? r[0] : r[1]);
+}
+
 // Epilogue on the accumulators in registers (see the comment above).
 // TAB_LDS: the RoPE table rows of the tile are staged in LDS at rope_tab
 // (given whenever the tile has rotated columns).
@@ -162,7 +170,24 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
                                               int tile_n, int wm, int wn, int l32, int hb,
                                               const char* rope_tab = nullptr) {
   const int row_base = m0 + wm * WM + 4 * hb;
-  if constexpr (EPI == EPI_GEGLU) {
+  if constexpr (EPI == EPI_GEGLU && TJ == 1) {
+    // one 32-column block (see mfma_w_row): lane c < 16 holds the input of
+    // output tile_n * BN / 2 + wn * WN / 2 + c, lane c + 16 its gate
+    static_assert(WN == 32, "GEGLU with one column block per wave");
+    OutT* out = static_cast<OutT*>(g.out);
+    const bool hi = l32 >= 16;
+    const int col = tile_n * (BN / 2) + wn * (WN / 2) + (l32 & 15);
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float own = acc[i][0][e];
+        const float gate = swap16(own, hi);  // every lane takes part
+        const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
+        if (!hi && m < g.M && col < g.N)
+          store_f32(out + static_cast<int64_t>(m) * g.ldo + col, gelu_out<OutT>(own) * gate);
+      }
+  } else if constexpr (EPI == EPI_GEGLU) {
     OutT* out = static_cast<OutT*>(g.out);
     const int c0 = tile_n * (BN / 2) + wn * (WN / 2) + l32;
 #pragma unroll
@@ -1194,6 +1219,19 @@ void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
 #ifndef SJH_GEMM_SMALL
 #define SJH_GEMM_SMALL 64, 64, 2, 1, 4, 64
 #endif
+// Up to SJH_SMALL32_MAX_M rows (batch-1 latency), the GEGLU and plain
+// products take 32-column tiles: a CU streams W at ~25 GB/s at most, so half
+// the W rows per workgroup on twice the workgroups shortens the K loop
+// (batch-1 Wi + GEGLU 10.2 -> 8.1 us per launch).  A GEGLU tile's input and
+// gate rows meet in the epilogue by a lane swap.  The RoPE product keeps
+// 64-column tiles: with its rotation pairs one per lane, its epilogue does
+// half the work per output (8.3 us against 9.0 with paired 32-column tiles).
+#ifndef SJH_GEMM_SMALL32
+#define SJH_GEMM_SMALL32 64, 32, 2, 1, 4, 64
+#endif
+#ifndef SJH_SMALL32_MAX_M
+#define SJH_SMALL32_MAX_M 256
+#endif
 #ifndef SJH_SPLITK_MAX_M
 #define SJH_SPLITK_MAX_M 256
 #endif
@@ -1217,6 +1255,10 @@ void launch_mfma(const GemmArgs& g, hipStream_t st) {
     launch_mfma_epi<SJH_GEMM_BIG>(g, st);
   else if (g.M >= 1024)
     launch_mfma_epi<SJH_GEMM_MID>(g, st);
+  else if (g.M <= SJH_SMALL32_MAX_M && g.epi == EPI_GEGLU)
+    launch_mfma_tile<SJH_GEMM_SMALL32, EPI_GEGLU>(g, st);
+  else if (g.M <= SJH_SMALL32_MAX_M && g.epi == EPI_STORE)
+    launch_mfma_tile<SJH_GEMM_SMALL32, EPI_STORE>(g, st);
   else
     launch_mfma_epi<SJH_GEMM_SMALL>(g, st);
 }
