@@ -337,30 +337,52 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
     else
       body(std::true_type{});
   } else {
-    OutT* out = static_cast<OutT*>(g.out);
-    const int c0 = tile_n * BN + wn * WN + l32;
+    // out = act(acc + bias).  Addresses are the wave's uniform corner plus
+    // one 32-bit byte offset per access; the activation and the bounds checks
+    // (rows or columns of the wave past M or N) are chosen once per wave.
+    constexpr int EB = sizeof(OutT);
+    const int c0 = tile_n * BN + wn * WN;
+    const int rw = m0 + wm * WM;  // the wave's first row
+    const char* ow = reinterpret_cast<const char*>(static_cast<OutT*>(g.out) + static_cast<int64_t>(rw) * g.ldo + c0);
+    const uint32_t ldb = static_cast<uint32_t>(g.ldo) * EB;
+    const uint32_t lo = 4 * hb * ldb + l32 * EB;
+    const bool rfull = rw + WM <= g.M, cfull = c0 + WN <= g.N;  // uniform
     float bv[TJ];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) bv[j] = (g.bias && c0 + j * 32 < g.N) ? g.bias[c0 + j * 32] : 0.f;
+    for (int j = 0; j < TJ; ++j) bv[j] = g.bias ? g.bias[min(c0 + j * 32 + l32, g.N - 1)] : 0.f;
+    auto body = [&](auto checked, auto act_tag) {
+      constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
-        if (m >= g.M) continue;
-        OutT* orow = out + static_cast<int64_t>(m) * g.ldo;
+        for (int e = 0; e < 16; ++e) {
+          const int r = i * 32 + 8 * (e >> 2) + (e & 3);
+          if (decltype(checked)::value && rw + r + 4 * hb >= g.M) continue;
+          char* orow = const_cast<char*>(ow) + static_cast<uint32_t>(r * ldb + lo);
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-          const int col = c0 + j * 32;
-          if (col >= g.N) continue;
-          float v = acc[i][j][e] + bv[j];
-          if (g.act == 1)
-            v = gelu_out<OutT>(v);
-          else if (g.act == 2)
-            v = fmaxf(v, 0.f);
-          store_f32(orow + col, v);
+          for (int j = 0; j < TJ; ++j) {
+            if (decltype(checked)::value && c0 + j * 32 + l32 >= g.N) continue;
+            float v = acc[i][j][e] + bv[j];
+            if constexpr (ACT == 1)
+              v = gelu_out<OutT>(v);
+            else if constexpr (ACT == 2)
+              v = fmaxf(v, 0.f);
+            store_f32(reinterpret_cast<OutT*>(orow + j * 32 * EB), v);
+          }
         }
-      }
+    };
+    auto by_act = [&](auto checked) {
+      if (g.act == 1)
+        body(checked, std::integral_constant<int, 1>{});
+      else if (g.act == 2)
+        body(checked, std::integral_constant<int, 2>{});
+      else
+        body(checked, std::integral_constant<int, 0>{});
+    };
+    if (rfull && cfull)
+      by_act(std::false_type{});
+    else
+      by_act(std::true_type{});
   }
 }
 

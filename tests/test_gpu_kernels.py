@@ -55,8 +55,10 @@ def rnd(rng, shape, scale=1.0):
 # (4500, 512, 64) and (4200, 256, 128) take the persistent kernel (M >= 4096)
 # with fewer K steps per tile than its load ring keeps in flight: the ring then
 # moves on to the next tile during the prologue (regression case)
+# (130, 200, 128) and (600, 200, 128): a last column tile past N on the 64x32
+# and 64x64 tiles (the store epilogue's bounds-checked body)
 @pytest.mark.parametrize("M,N,K", [(300, 256, 128), (1, 128, 64), (130, 384, 192), (640, 2304, 768),
-                                   (4500, 512, 64), (4200, 256, 128)])
+                                   (4500, 512, 64), (4200, 256, 128), (130, 200, 128), (600, 200, 128)])
 @pytest.mark.parametrize("act", [0, 1, 2])
 def test_gemm_bf16_mfma(orc, M, N, K, act):
     print(f"gemm bf16 M={M} N={N} K={K} act={act}", flush=True)
