@@ -545,17 +545,45 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_kernel(GemmArgs 
     // epilogue.  The tile holds every W row its outputs need (GEGLU input and
     // gate rows, both halves of a RoPE head).
     float* part = g.partial + static_cast<int64_t>(blockIdx.y) * g.part_rows * g.n_w;
-    const int row_base = m0 + wm * TT::WM + 4 * hb;
+    if constexpr (EPI != EPI_GEGLU) {
+      // W row = output column: the wave's uniform corner plus one 32-bit
+      // byte offset per store; the bounds checks only where the wave's rows
+      // or columns run past M or N
+      const int rw = m0 + wm * TT::WM, c0 = tile_n * BN + wn * TT::WN;
+      char* pw = reinterpret_cast<char*>(part + static_cast<int64_t>(rw) * g.n_w + c0);
+      const uint32_t ldb = static_cast<uint32_t>(g.n_w) * 4u;
+      const uint32_t lo = 4 * hb * ldb + l32 * 4;
+      auto body = [&](auto checked) {
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int64_t wr = mfma_w_row<BN, TT::WN, EPI>(g, tile_n, wn * TT::WN + j * 32 + l32);
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int i = 0; i < TI; ++i)
+          for (int e = 0; e < 16; ++e) {
+            const int r = i * 32 + 8 * (e >> 2) + (e & 3);
+            if (decltype(checked)::value && rw + r + 4 * hb >= g.M) continue;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
-          if (m < g.M) part[static_cast<int64_t>(m) * g.n_w + wr] = acc[i][j][e];
-        }
+            for (int j = 0; j < TJ; ++j) {
+              if (decltype(checked)::value && c0 + j * 32 + l32 >= g.n_w) continue;
+              *reinterpret_cast<float*>(pw + static_cast<uint32_t>(r * ldb + lo) + j * 128) = acc[i][j][e];
+            }
+          }
+      };
+      if (rw + TT::WM <= g.M && c0 + TT::WN <= g.n_w)
+        body(std::false_type{});
+      else
+        body(std::true_type{});
+    } else {
+      const int row_base = m0 + wm * TT::WM + 4 * hb;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int64_t wr = mfma_w_row<BN, TT::WN, EPI>(g, tile_n, wn * TT::WN + j * 32 + l32);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int m = row_base + i * 32 + 8 * (e >> 2) + (e & 3);
+            if (m < g.M) part[static_cast<int64_t>(m) * g.n_w + wr] = acc[i][j][e];
+          }
+      }
     }
   }
 }
