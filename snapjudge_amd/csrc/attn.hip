@@ -92,7 +92,9 @@ __device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
 
 // Register budget for three workgroups per CU (168 VGPRs, 3 waves per SIMD):
 // a third wave per SIMD lets softmax VALU work, MFMAs and LDS reads of
-// different waves overlap.  PRE: q holds q * scale * log2 e (AttnArgs::
+// different waves overlap.  (The pre-scaled kernel spills 3 VGPRs on the
+// max-rule rerun only, past the redo vote; the common path has no scratch
+// access.)  PRE: q holds q * scale * log2 e (AttnArgs::
 // q_log2_scaled).
 // One work item: queries [q0, q0 + kQ) of head h of the sequence whose rows
 // start at row0 (q0 < qlen).
@@ -217,11 +219,8 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
         s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[jb], 0, 0, 0);
       }
     }
-    // The last tile of full attention in the offset-free pass needs no mask:
-    // its keys past klen have zero K and V rows, so each adds 2^0 = 1 to the
-    // lane's weight sum and nothing to O; the sum gives them back below.
-    constexpr bool kZeroRows = NOMAX && MASK == 1;
-    if constexpr (MASK != 0 && !kZeroRows) {
+    static_assert(!(NOMAX && MASK == 1), "the offset-free pass takes the last tile unmasked");
+    if constexpr (MASK != 0) {
       // key of element (jb, e) is kt + 4*hb + 32*jb + 8*(e/4) + e%4
       const int lo = qlo - kt - 4 * hb, hi = qhi - kt - 4 * hb;
 #pragma unroll
@@ -308,14 +307,6 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
         }
       }
-    if constexpr (kZeroRows) {
-      // this lane's keys are kt + 8g + 4hb + [0, 4), g = 0..7; with rr =
-      // klen - kt - 4hb, those at or past klen are all of groups g > rr / 8
-      // and 4 - rr % 8 (if positive) of group rr / 8
-      const int rr = klen - kt - 4 * hb;
-      const int n_out = rr <= 0 ? 32 : rr >= 60 ? 0 : 4 * (7 - (rr >> 3)) + max(0, 4 - (rr & 7));
-      l_i -= static_cast<float>(n_out);
-    }
   };
 
   // ST: the ring slot of tile t when the caller knows it (t % kNS), so the
@@ -350,16 +341,25 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     using I0 = std::integral_constant<int, 0>;
     using Idyn = std::integral_constant<int, -1>;
     static_assert(kNS == 2, "the interior loop is unrolled by the ring depth");
+    // The offset-free pass of full attention takes every tile through the
+    // interior body, the last one too: its keys past klen have zero K and V
+    // rows (the descriptors end at the last key), so each adds 2^0 = 1 to
+    // the weight sum and nothing to O; the caller gives them back.
+    constexpr bool NOMAX = decltype(nomax_tag)::value;
+    const bool all_plain = NOMAX && a.window == 0;  // uniform
+    const int n_int = all_plain ? ntiles : n_plain;
     int t = 0;
-    for (; t + 1 < n_plain; t += 2) {  // t is even: slots 0 then 1
+    for (; t + 1 < n_int; t += 2) {  // t is even: slots 0 then 1
       step(t, I0{}, nomax_tag, I0{});
       step(t + 1, I0{}, nomax_tag, std::integral_constant<int, 1>{});
     }
-    for (; t < n_plain; ++t) step(t, I0{}, nomax_tag, Idyn{});
-    if (a.window > 0)
+    for (; t < n_int; ++t) step(t, I0{}, nomax_tag, Idyn{});
+    if (a.window > 0) {
       for (; t < ntiles; ++t) step(t, std::integral_constant<int, 2>{}, nomax_tag, Idyn{});
-    else
-      for (; t < ntiles; ++t) step(t, std::integral_constant<int, 1>{}, nomax_tag, Idyn{});
+    } else {
+      if constexpr (!NOMAX)
+        for (; t < ntiles; ++t) step(t, std::integral_constant<int, 1>{}, nomax_tag, Idyn{});
+    }
     l_i += l_j;
     return l_i + __shfl_xor(l_i, 32, 64);
   };
@@ -375,6 +375,15 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     int* redo = reinterpret_cast<int*>(smem + kNS * kStage);
     if (tid == 0) *redo = 0;  // ordered before other waves' writes by pass 1's barriers
     l_tot = pass(std::true_type{});
+    if (a.window == 0 && ntiles > 0) {  // uniform
+      // the keys at or past klen in the last tile, each counted once with
+      // weight 1 (both wave halves' keys: kt + 8g + 4hb + [0, 4), g = 0..7;
+      // with rr = klen - kt - 4hb, groups g > rr / 8 and 4 - rr % 8 of group
+      // rr / 8 lie past the end)
+      auto n_out = [](int rr) { return rr <= 0 ? 32 : rr >= 60 ? 0 : 4 * (7 - (rr >> 3)) + max(0, 4 - (rr & 7)); };
+      const int rr = klen - (klo + (ntiles - 1) * kKey);
+      l_tot -= static_cast<float>(n_out(rr) + n_out(rr - 4));
+    }
     if (ntiles > 0) {  // uniform
       const bool bad = wave_active && qi < qlen && qhi > qlo && !(l_tot >= 0x1p-60f && l_tot <= 0x1p64f);
       if (__any(bad) && lane == 0) *redo = 1;
