@@ -8,8 +8,9 @@
 // S^T = K . Q^T with
 // v_mfma_f32_32x32x16_bf16 (the query is the MFMA column, so each lane owns
 // one query and 32 of the tile's keys), does the online-softmax update in
-// registers (row max over its own values plus one cross-half exchange; exp2
-// with the 1/sqrt(Dh)*log2(e) scale folded in), and accumulates
+// registers (exp2 of log2-domain logits; a first pass without any running
+// max, checked afterwards, else the max rule with one cross-half exchange
+// for the row max), and accumulates
 // O^T += V^T . P^T.  The accumulator of S^T is already laid out as the B
 // operand of the second MFMA once the key order inside a 16-key step is taken
 // as the MFMA's k order, so P never leaves registers; the V^T operand comes
@@ -133,8 +134,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
   // Groups i = 0, 1 are K rows, 2, 3 V rows.  The loads go through buffer
   // descriptors based at the sequence's first K and V rows: a full tile is
   // the tile's row offset (scalar) plus the lane's fixed byte offset, with no
-  // per-lane address arithmetic; only a tile that runs past klen clamps its
-  // rows one by one (32-bit lane offsets from the sequence's base).
+  // per-lane address arithmetic; a tile that runs past klen takes 32-bit
+  // lane offsets from the sequence's base, and its rows past the last key
+  // fall outside the descriptors and load as zeros.
   const int lrow = lane >> 3, cslot = lane & 7;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   uint32_t goff[4];
