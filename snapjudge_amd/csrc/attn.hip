@@ -98,10 +98,12 @@ __device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
 // access.)  PRE: q holds q * scale * log2 e (AttnArgs::
 // q_log2_scaled).
 // One work item: queries [q0, q0 + kQ) of head h of the sequence whose rows
-// start at row0 (q0 < qlen).
+// start at row0 (q0 < qlen).  half 0: all keys; 1: keys [0, mid), 2: keys
+// [mid, klen) with mid = klen / 2 rounded up to a whole tile (full attention
+// only), the unnormalised result going to part (kAttnPartFloats floats).
 template <bool PRE>
 __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t row0, int qlen, int klen,
-                                          int h, int q0) {
+                                          int h, int q0, int half = 0, float* part = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hb = lane >> 5;
 
@@ -122,6 +124,12 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
   if (a.window > 0) {
     klo = max(0, q0 - a.window);
     khi = min(klen, q0 + kQ - 1 + a.window + 1);
+  } else if (half > 0) {
+    const int mid = ((klen + 1) / 2 + kKey - 1) / kKey * kKey;
+    if (half == 1)
+      khi = mid;
+    else
+      klo = mid;
   }
   const int qlo = a.window > 0 ? max(0, qi - a.window) : 0;
   const int qhi = a.window > 0 ? min(klen, qi + a.window + 1) : klen;
@@ -378,7 +386,8 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     if (tid == 0) *redo = 0;  // ordered before other waves' writes by pass 1's barriers
     l_tot = pass(std::true_type{});
     if (a.window == 0 && ntiles > 0) {  // uniform
-      // the keys at or past klen in the last tile, each counted once with
+      // the keys at or past klen in the last tile (none before a half item's
+      // middle), each counted once with
       // weight 1 (both wave halves' keys: kt + 8g + 4hb + [0, 4), g = 0..7;
       // with rr = klen - kt - 4hb, groups g > rr / 8 and 4 - rr % 8 of group
       // rr / 8 lie past the end)
@@ -394,6 +403,25 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     }
   } else {
     l_tot = pass(std::false_type{});
+  }
+  if (half > 0) {
+    // a half item: O^T as accumulated, then per query the weight sum and the
+    // softmax offset (log2 domain; 0 for the offset-free pass), rows past
+    // q_len left out
+    if (qi < qlen) {
+      const int ql = wave * 32 + l32;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq)
+          *reinterpret_cast<f32x4_t*>(part + ql * 64 + db * 32 + 8 * gq + 4 * hb) =
+              (f32x4_t){o[db][4 * gq], o[db][4 * gq + 1], o[db][4 * gq + 2], o[db][4 * gq + 3]};
+      if (hb == 0) {
+        part[kQ * 64 + ql] = l_tot;
+        part[kQ * 64 + kQ + ql] = m_i == -INFINITY ? 0.f : m_i;
+      }
+    }
+    return;
   }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qi < qlen) {
@@ -418,7 +446,15 @@ __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
   if (a.items) {  // the work list: this workgroup's slot
     const int4 m = reinterpret_cast<const int4*>(a.items)[blockIdx.x];
     if (m.y <= 0) return;  // an empty slot (uniform over the workgroup)
-    attn_item<PRE>(a, smem, m.x, m.y, m.z, m.w & 0xffff, static_cast<int>(static_cast<uint32_t>(m.w) >> 16) * kQ);
+    const int q0 = static_cast<int>(static_cast<uint32_t>(m.w) >> 16) * kQ;
+    if (m.w & 0x8000) {  // a half item of the key split: its pair's partials
+      const int half = (m.w >> 14) & 1;
+      const int pair = a.items[4 * a.n_slots + blockIdx.x];
+      float* part = a.part + (2 * static_cast<int64_t>(pair) + half) * kAttnPartFloats;
+      attn_item<PRE>(a, smem, m.x, m.y, m.z, m.w & 0x3fff, q0, 1 + half, part);
+    } else {
+      attn_item<PRE>(a, smem, m.x, m.y, m.z, m.w & 0x3fff, q0);
+    }
     return;
   }
   // Workgroup -> (sequence, head, query block).  Hardware hands workgroup i
@@ -451,35 +487,111 @@ __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
   attn_item<PRE>(a, smem, row0, qlen, klen, h, q0);
 }
 
+// First rank of the key-split tail (Bb: none): the smallest rank z, at a
+// change of length (rank z - 1 longer), such that the sequences from z on
+// hold at most a quarter of the batch's query blocks and each at least
+// kAttnSplitMinKeys keys.  Empty sequences (ranked last) are passed over.
+__device__ int attn_split_rank(const int32_t* table, int Bb) {
+  const int32_t* qbp = table + seq_table_qbp(Bb);
+  const int32_t* meta = table + seq_table_meta(Bb);
+  const int64_t qb_all = qbp[Bb];
+  int rs = Bb;
+  for (int z = Bb - 1; z >= 0; --z) {
+    const int n = meta[4 * z + 1];
+    if (n == 0) continue;
+    if (4 * (qb_all - qbp[z]) > qb_all || meta[4 * z + 2] < kAttnSplitMinKeys) break;
+    if (z == 0 || meta[4 * (z - 1) + 1] != n) rs = z;
+  }
+  return rs;
+}
+
+// Item i (< H * qbp[Bb]) of the batch's order: sequence z (rank), head h and
+// query block qb, z by bisection of the table's query-block prefix.
+__device__ void attn_item_of(const int32_t* qbp, int Bb, int H, int64_t i, int& z, int& h, int& qb) {
+  int lo = 0, hi = Bb;  // H * qbp[lo] <= i < H * qbp[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (static_cast<int64_t>(H) * qbp[mid] <= i)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  const int nb = qbp[lo + 1] - qbp[lo];  // >= 1: item i lies in sequence lo's range
+  const int r = static_cast<int>(i - static_cast<int64_t>(H) * qbp[lo]);
+  z = lo;
+  h = r / nb;
+  qb = r - h * nb;
+}
+
 // Work list (launch_attn_items): one thread per slot.  Slot (workgroup) s
 // runs on XCD s % 8 and is place pos = s / 8 of that XCD's list, which holds
 // the items of runs x, x + 8, x + 16, ... (runs of kAttnRun items of the
-// batch's item order).  Item i's sequence z is found by bisection of the
-// table's query-block prefix.
+// batch's item order).  With split, the items of the tail ranks follow the
+// others as half items, both halves of an item side by side.
 __global__ __launch_bounds__(256) void attn_items_kernel(const int32_t* table, int Bb, int H, int n_slots,
-                                                         int32_t* items) {
+                                                         int split, int32_t* items) {
   const int s = blockIdx.x * 256 + threadIdx.x;
   if (s >= n_slots) return;
   const int32_t* qbp = table + seq_table_qbp(Bb);
   const int32_t* meta = table + seq_table_meta(Bb);
   const int pos = s >> 3;
   const int64_t i = (static_cast<int64_t>(pos / kAttnRun) * 8 + (s & 7)) * kAttnRun + pos % kAttnRun;
+  const int rs = split ? attn_split_rank(table, Bb) : Bb;
+  const int64_t n_whole = static_cast<int64_t>(H) * qbp[rs];
+  const int64_t n_half = 2 * static_cast<int64_t>(H) * (qbp[Bb] - qbp[rs]);
   int4 out = {0, 0, 0, 0};
-  if (i < static_cast<int64_t>(H) * qbp[Bb]) {
-    int lo = 0, hi = Bb;  // H * qbp[lo] <= i < H * qbp[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (static_cast<int64_t>(H) * qbp[mid] <= i)
-        lo = mid;
-      else
-        hi = mid;
+  int pair = 0;
+  if (i < n_whole + n_half) {
+    const bool halves = i >= n_whole;
+    int z, h, qb;
+    attn_item_of(qbp, Bb, H, halves ? n_whole + ((i - n_whole) >> 1) : i, z, h, qb);
+    int w = h | (qb << 16);
+    if (halves) {
+      w |= 0x8000 | (static_cast<int>((i - n_whole) & 1) << 14);
+      pair = static_cast<int>((i - n_whole) >> 1);
     }
-    const int nb = qbp[lo + 1] - qbp[lo];  // >= 1: item i lies in sequence lo's range
-    const int r = static_cast<int>(i - static_cast<int64_t>(H) * qbp[lo]);
-    const int h = r / nb, qb = r - h * nb;
-    out = (int4){meta[4 * lo], meta[4 * lo + 1], meta[4 * lo + 2], h | (qb << 16)};
+    out = (int4){meta[4 * z], meta[4 * z + 1], meta[4 * z + 2], w};
   }
   reinterpret_cast<int4*>(items)[s] = out;
+  if (split) items[4 * static_cast<int64_t>(n_slots) + s] = pair;
+}
+
+// Merge of the split items (launch_attn_merge): workgroup p = pair p; thread
+// t takes dims 4 (t % 16) + [0, 4) of queries t / 16 + 16 r, r < 8 (a row's
+// 16 threads read and write it contiguously).
+__global__ __launch_bounds__(256) void attn_merge_kernel(const int32_t* table, int Bb, int H, const float* part,
+                                                         bf16_t* o, int64_t ld_o) {
+  const int32_t* qbp = table + seq_table_qbp(Bb);
+  const int32_t* meta = table + seq_table_meta(Bb);
+  const int rs = attn_split_rank(table, Bb);
+  const int64_t n_whole = static_cast<int64_t>(H) * qbp[rs];
+  const int64_t p = blockIdx.x;
+  if (n_whole + p >= static_cast<int64_t>(H) * qbp[Bb]) return;  // uniform
+  int z, h, qb;
+  attn_item_of(qbp, Bb, H, n_whole + p, z, h, qb);
+  const int64_t row0 = meta[4 * z];
+  const int qlen = meta[4 * z + 1];
+  const float* p1 = part + 2 * p * kAttnPartFloats;
+  const float* p2 = p1 + kAttnPartFloats;
+  const int c = threadIdx.x & 15;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int q = (threadIdx.x >> 4) + 16 * r;
+    const int qi = qb * kQ + q;
+    if (qi >= qlen) break;
+    const float m1 = p1[kQ * 64 + kQ + q], m2 = p2[kQ * 64 + kQ + q];
+    const float mx = fmaxf(m1, m2);
+    const float w1 = __builtin_amdgcn_exp2f(m1 - mx), w2 = __builtin_amdgcn_exp2f(m2 - mx);
+    const float l = p1[kQ * 64 + q] * w1 + p2[kQ * 64 + q] * w2;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const float s1 = w1 * inv, s2 = w2 * inv;
+    const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(p1 + q * 64 + 4 * c);
+    const f32x4_t x2 = *reinterpret_cast<const f32x4_t*>(p2 + q * 64 + 4 * c);
+    u32x2_t w;
+    w[0] = pack_bf16x2(x1[0] * s1 + x2[0] * s2, x1[1] * s1 + x2[1] * s2);
+    w[1] = pack_bf16x2(x1[2] * s1 + x2[2] * s2, x1[3] * s1 + x2[3] * s2);
+    *reinterpret_cast<u32x2_t*>(o + (row0 + qi) * ld_o + h * 64 + 4 * c) = w;
+  }
 }
 
 // ------------------------------------------------------------------ generic
@@ -596,6 +708,8 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
               a.ld_o >= a.H * a.Dh,
           "attention: row stride < H*Dh");
   require(a.window >= 0, "attention: negative window");
+  require(!a.part || (a.items && a.window == 0 && (reinterpret_cast<uintptr_t>(a.part) & 15u) == 0),
+          "attention: split items need the work list, full attention and 16-byte aligned partials");
   require(!a.seq_meta || (a.seq_start && a.q_len && (reinterpret_cast<uintptr_t>(a.seq_meta) & 15u) == 0),
           "attention: seq_meta needs the varlen layout and 16-byte alignment");
   const bool mfma = a.dtype == DT_BF16 && a.Dh == 64 && a.ld_q % 8 == 0 && a.ld_k % 8 == 0 &&
@@ -630,24 +744,52 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
   check_launch("attn_generic");
 }
 
-int attn_item_slots(int Tb, int Bb, int H) {
-  require(Tb >= 0 && Bb >= 0 && H > 0, "attention items: bad shape");
-  // sum over sequences of ceil(n / kAttnQ) <= (T + (kAttnQ - 1) B) / kAttnQ
-  const int64_t items = static_cast<int64_t>(H) * ((static_cast<int64_t>(Tb) + (kAttnQ - 1) * int64_t{Bb} + kAttnQ - 1) / kAttnQ);
+namespace {
+// query blocks of any batch of at most Tb rows in at most Bb sequences:
+// sum over sequences of ceil(n / kAttnQ) <= (T + (kAttnQ - 1) B) / kAttnQ
+int64_t max_query_blocks(int Tb, int Bb) {
+  require(Tb >= 0 && Bb >= 0, "attention items: bad shape");
+  return (static_cast<int64_t>(Tb) + (kAttnQ - 1) * int64_t{Bb} + kAttnQ - 1) / kAttnQ;
+}
+}  // namespace
+
+int attn_split_pairs(int Tb, int Bb, int H) {
+  require(H > 0, "attention items: bad shape");
+  // the tail holds at most a quarter of the query blocks
+  const int64_t pairs = static_cast<int64_t>(H) * (max_query_blocks(Tb, Bb) / 4);
+  require(pairs < (int64_t{1} << 28), "attention items: too many");
+  return static_cast<int>(pairs);
+}
+
+int attn_item_slots(int Tb, int Bb, int H, bool split) {
+  require(H > 0, "attention items: bad shape");
+  int64_t items = static_cast<int64_t>(H) * max_query_blocks(Tb, Bb);
+  if (split) items += attn_split_pairs(Tb, Bb, H);  // a split item takes two slots
   const int64_t slots = 8 * ((items + 8 * kAttnRun - 1) / (8 * kAttnRun)) * kAttnRun;
   require(slots < (int64_t{1} << 30), "attention items: too many");
   return static_cast<int>(slots);
 }
 
-void launch_attn_items(const int32_t* table, int Bb, int H, int n_slots, int32_t* items, hipStream_t st) {
+void launch_attn_items(const int32_t* table, int Bb, int H, int n_slots, bool split, int32_t* items,
+                       hipStream_t st) {
   if (n_slots <= 0) return;
   require(table && items && (reinterpret_cast<uintptr_t>(items) & 15u) == 0 && Bb >= 1 && H >= 1 &&
-              H < 65536 && n_slots % 8 == 0,
+              H < 16384 && n_slots % 8 == 0,
           "attention items: bad arguments");
   // (the caller keeps every sequence below 65536 query blocks: the item
-  // holds the block index in 16 bits)
-  attn_items_kernel<<<(n_slots + 255) / 256, 256, 0, st>>>(table, Bb, H, n_slots, items);
+  // holds the block index in 16 bits, the head in 14)
+  attn_items_kernel<<<(n_slots + 255) / 256, 256, 0, st>>>(table, Bb, H, n_slots, split ? 1 : 0, items);
   check_launch("attn_items");
+}
+
+void launch_attn_merge(const int32_t* table, int Bb, int H, int max_pairs, const float* part, void* o,
+                       int64_t ld_o, hipStream_t st) {
+  if (max_pairs <= 0) return;
+  require(table && part && o && Bb >= 1 && H >= 1 && ld_o >= 64 * int64_t{H} && ld_o % 4 == 0 &&
+              (reinterpret_cast<uintptr_t>(part) & 15u) == 0 && (reinterpret_cast<uintptr_t>(o) & 7u) == 0,
+          "attention merge: bad arguments");
+  attn_merge_kernel<<<max_pairs, 256, 0, st>>>(table, Bb, H, part, static_cast<bf16_t*>(o), ld_o);
+  check_launch("attn_merge");
 }
 
 }  // namespace sjh

@@ -460,6 +460,8 @@ void Engine::stage_weights(const ModelSource& s) {
     L.window = s0.window;
     L.sliding = s0.sliding;
   }
+  attn_split_ = max_len_ >= kAttnSplitMinKeys;
+  for (const auto& L : layers_) attn_split_ = attn_split_ && L.window == 0;
 
   if (lora_r_ > 0) {
     lora_a_ = put_f32(s.lora_a, static_cast<int64_t>(lora_r_) * D, "lora_a");
@@ -639,8 +641,10 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   tok_pos_.ensure(t * 4);
   tok_seq_.ensure(t * 4);
   seqinfo_.ensure(seq_table_ints(std::max(nB, 1)) * 4);
-  const int n_items = attn_item_slots(nT, nB, H_);
-  attn_items_.ensure(static_cast<size_t>(n_items) * 16);
+  const int n_items = attn_item_slots(nT, nB, H_, attn_split_);
+  attn_items_.ensure(attn_items_ints(n_items) * 4);
+  const int n_pairs = attn_split_ ? attn_split_pairs(nT, nB, H_) : 0;
+  if (n_pairs > 0) attn_part_.ensure(static_cast<size_t>(n_pairs) * 2 * kAttnPartFloats * 4);
   X_.ensure(t * D * 4);
   Y_.ensure(t * D * as);
   QKV_.ensure(t * 3 * D * as);
@@ -666,6 +670,8 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   ws_.partial_cap = static_cast<int64_t>(splitk_.bytes() / 4);
   ws_.attn_items = attn_items_.as<int32_t>();
   ws_.attn_slots_cap = n_items;
+  ws_.attn_part = n_pairs > 0 ? attn_part_.as<float>() : nullptr;
+  ws_.attn_pairs_cap = n_pairs;
   ++ws_gen_;
   for (auto& kv : graphs_)
     if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
@@ -842,12 +848,16 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
 
   launch_token_index(seq_start, q_len, Bb, w.tok_pos, w.tok_seq, st);
   // the attention work list of the batch, when the bf16 head_dim-64 kernel runs
-  // (the list holds a query block's index in 16 bits)
+  // (the list holds a query block's index in 16 bits); the shortest
+  // sequences' items split by keys when the batch may hold such (launch_attn_items)
   const bool attn_list = adt == DT_BF16 && Dh_ == 64 && w.attn_items && p.max_qb <= 65536 * kAttnQ;
-  const int attn_slots = attn_list ? attn_item_slots(T, Bb, H_) : 0;
+  const bool attn_split = attn_list && w.attn_part && p.max_qb >= kAttnSplitMinKeys;
+  const int attn_slots = attn_list ? attn_item_slots(T, Bb, H_, attn_split) : 0;
+  const int attn_pairs = attn_split ? attn_split_pairs(T, Bb, H_) : 0;
   if (attn_list) {
-    require(attn_slots <= w.attn_slots_cap, "attention work list: workspace too small");
-    launch_attn_items(si, Bb, H_, attn_slots, w.attn_items, st);
+    require(attn_slots <= w.attn_slots_cap && attn_pairs <= w.attn_pairs_cap,
+            "attention work list: workspace too small");
+    launch_attn_items(si, Bb, H_, attn_slots, attn_split, w.attn_items, st);
   }
 
   // src/model.cpp:332-340: X = LN(emb[ids]); layer 0 reads X itself.  BERT
@@ -980,8 +990,12 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       if (attn_list) {
         a.items = w.attn_items;
         a.n_slots = attn_slots;
+        if (attn_split) a.part = w.attn_part;
       }
-      attn("attention", a, st);
+      prof_begin(st);
+      launch_attn(a, st);
+      if (attn_split) launch_attn_merge(si, Bb, H_, attn_pairs, w.attn_part, O, D, st);
+      prof_end("attention", st);
     }
     {  // X += O . Wo^T (src/model.cpp:389-391)
       GemmArgs g;

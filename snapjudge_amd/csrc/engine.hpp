@@ -99,6 +99,8 @@ struct Ws {
   int64_t partial_cap = 0;   // floats
   int32_t* attn_items = nullptr;  // attention work list (AttnArgs::items)
   int attn_slots_cap = 0;         // its slots
+  float* attn_part = nullptr;     // partials of key-split items (AttnArgs::part), or none
+  int attn_pairs_cap = 0;         // split items they hold
 };
 
 class Engine {
@@ -215,6 +217,7 @@ class Engine {
   int D_ = 0, H_ = 0, Dh_ = 0, F_ = 0, V_ = 0, nlayers_ = 0, max_pos_ = 0;
   int n_act_ = 0, head_layers_ = 0, lora_r_ = 0, max_len_ = 0;
   float eps_ = 1e-5f;
+  bool attn_split_ = false;  // every layer has full attention and sequences can reach kAttnSplitMinKeys
   int arch_ = ARCH_MODERNBERT;  // ModernBERT (DecisionModel) or BERT (SjModel)
   int act_head_ = ACT_MLP;
   int head_ff_ = 0, head_act_ = 2;
@@ -238,6 +241,7 @@ class Engine {
   std::vector<int32_t> tail_hidx_;  // host copy of the head tail's row indices
   DevBuf splitk_;  // split-K partial sums for short batches (GemmArgs::partial)
   DevBuf attn_items_;  // attention work list (AttnArgs::items)
+  DevBuf attn_part_;   // partials of key-split attention items (AttnArgs::part)
   Ws ws_;          // views of the buffers above
   DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_lg_, tail_ain_, tail_ah_,
       tail_ao_, tail_act_;

@@ -155,6 +155,9 @@ struct AttnArgs {
   // The grid is then n_slots workgroups whatever B and max_q say.
   const int* items = nullptr;
   int n_slots = 0;
+  // Partials of the work list's key-split items (launch_attn_items with
+  // split): kAttnPartFloats floats per half item, merged by launch_attn_merge.
+  float* part = nullptr;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);
 
@@ -168,11 +171,35 @@ void launch_attn(const AttnArgs& a, hipStream_t st);
 // empty workgroup for every block a shorter sequence lacks).
 constexpr int kAttnQ = 128;
 constexpr int kAttnRun = 4;
+//
+// Key split of the tail (full attention only): the shortest sequences, from
+// the first rank z whose length differs from rank z - 1's on, whose query
+// blocks are at most a quarter of the batch's and which each hold at least
+// kAttnSplitMinKeys keys, run every item as two half items over keys
+// [0, mid) and [mid, k_len), mid = k_len / 2 rounded up to 64 keys.  They
+// are the list's last items, the two halves of one item side by side; each
+// half leaves its unnormalised O^T, weight sums and softmax offsets in
+// AttnArgs::part (kAttnPartFloats floats at (2 pair + half) * kAttnPartFloats)
+// and launch_attn_merge writes the item's output rows.  The split depends
+// only on the batch's multiset of lengths (never on its order).
+constexpr int kAttnSplitMinKeys = 2048;
+constexpr int kAttnPartFloats = kAttnQ * 64 + 2 * kAttnQ;
 // Slots for any batch of at most Tb rows in at most Bb sequences (a multiple
-// of 8 * kAttnRun).
-int attn_item_slots(int Tb, int Bb, int H);
-// Fills items[0, n_slots) from the sequence table (its query-block prefix).
-void launch_attn_items(const int32_t* table, int Bb, int H, int n_slots, int32_t* items, hipStream_t st);
+// of 8 * kAttnRun), with room for the split's half items when split.
+int attn_item_slots(int Tb, int Bb, int H, bool split = false);
+// Item pairs a split can make for such a batch (the merge's grid).
+int attn_split_pairs(int Tb, int Bb, int H);
+// Ints of the list: n_slots int4 items, then (split) one pair index per slot.
+inline size_t attn_items_ints(int n_slots) { return 5u * static_cast<size_t>(n_slots); }
+// Fills items[0, n_slots) (and the pair indices when split) from the sequence
+// table (its query-block prefix).
+void launch_attn_items(const int32_t* table, int Bb, int H, int n_slots, bool split, int32_t* items,
+                       hipStream_t st);
+// Output rows of the split items: O = (2^(m1-M) O1 + 2^(m2-M) O2) /
+// (2^(m1-M) l1 + 2^(m2-M) l2), M = max(m1, m2), bf16 into o (row stride ld_o,
+// head h at column 64 h).  Workgroups past the batch's pairs return.
+void launch_attn_merge(const int32_t* table, int Bb, int H, int max_pairs, const float* part, void* o,
+                       int64_t ld_o, hipStream_t st);
 
 // Standalone RoPE on packed (q|k|v)(head)(dim) rows, position = pos[r]
 // (or r % L when pos is null), as src/tensor.cpp:257-279.

@@ -225,6 +225,34 @@ def test_more_than_256_sequences(orc):
     m.close()
 
 
+def test_attention_key_split_tail(orc):
+    # Lengths 8000, 6000, 2100, 2100: the two shortest rows hold 34 of the
+    # batch's 144 query blocks (at most a quarter) and at least 2048 keys
+    # each, so their attention items run as two key halves whose partials a
+    # merge kernel combines (the tied rows both split: the split never
+    # depends on the batch order).  Each split row against the oracle on the
+    # row alone; alone it runs unsplit (a batch of one), and the rounding of
+    # the two-half sum shows in the bits.  Reversing the batch permutes the
+    # outputs bit for bit.
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg4"], num_hidden_layers=2), seed=61)
+    cfg = synth.flat_cfg(rl, enc)
+    ids, mask, lens = synth.batch_with_lens(np.array([2100, 8000, 2100, 6000]), 8000, cfg["vocab_size"], seed=62)
+    m = sj.Model(w, cfg, precision=BF16)
+    h = m.encode(ids, mask)
+    om = orc.model(w, cfg)
+    for b in (0, 2):
+        ref = om.encode(ids[b:b + 1, :2100], mask[b:b + 1, :2100])[0]
+        err = float(np.abs(h[b, :2100] - ref).max())
+        alone = m.encode(ids[b:b + 1, :2100], mask[b:b + 1, :2100])[0]
+        print(f"split row {b} max|d|={err:.3g} alone {float(np.abs(alone - ref).max()):.3g}", flush=True)
+        assert err <= TOL[BF16]
+        assert not np.array_equal(alone, h[b, :2100])
+    hr = m.encode(ids[::-1].copy(), mask[::-1].copy())
+    assert np.array_equal(hr[::-1], h)
+    assert np.all(h[~mask.astype(bool)] == 0)
+    m.close()
+
+
 @pytest.fixture(scope="module")
 def cfg4(golden_dir):
     g = np.load(os.path.join(golden_dir, "cfg4_b4s8192.npz"))
