@@ -250,6 +250,14 @@ def test_attention_key_split_tail(orc):
     hr = m.encode(ids[::-1].copy(), mask[::-1].copy())
     assert np.array_equal(hr[::-1], h)
     assert np.all(h[~mask.astype(bool)] == 0)
+    # 8000, 2100, 2100, 2100: the three tied rows hold 51 of 114 blocks
+    # (more than a quarter) and no length change splits them off, so nothing
+    # splits and each 2100 row equals its run alone bit for bit (the GEMMs
+    # give the same bits for a row at any tile shape)
+    ids3, mask3, _ = synth.batch_with_lens(np.array([8000, 2100, 2100, 2100]), 8000, cfg["vocab_size"], seed=63)
+    h3 = m.encode(ids3, mask3)
+    for b in (1, 3):
+        assert np.array_equal(h3[b, :2100], m.encode(ids3[b:b + 1, :2100], mask3[b:b + 1, :2100])[0])
     m.close()
 
 
