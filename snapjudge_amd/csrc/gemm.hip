@@ -256,11 +256,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
     // head when j is even and dims [32, 64) when odd; its partner is j ^ 1.
     // Table entries of a group of RG rows are fetched together: from the
     // unit's table rows in LDS (rope_tab) or, without them, gathered through
-    // the positions (two memory round trips per group, not two per row).
+    // the positions (two memory round trips per group, not two per row; a
+    // wave with one 32-row block takes its 16 rows per lane in one group).
     // Addresses are the wave's uniform corner plus one 32-bit byte offset per
     // access; elements past M or N are skipped.
     static_assert(TJ % 2 == 0, "RoPE pairs need an even number of column blocks");
-    constexpr int RG = 8;
+    constexpr int RG = (!TAB_LDS && TI == 1) ? 16 : 8;
     constexpr int EB = sizeof(OutT);
     const int c0 = tile_n * BN + wn * WN;
     const int rw = m0 + wm * WM;  // the wave's first row
