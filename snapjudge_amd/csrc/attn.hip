@@ -59,9 +59,15 @@ __device__ __forceinline__ float wave_max32(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Chunk position of 16-byte chunk c of tile row r is c ^ kv_swz(r): 16
-// consecutive rows read at one logical chunk hit 16 distinct bank groups.
-__device__ __forceinline__ int kv_swz(int r) { return (r >> 1) & 7; }
+// Chunk position of 16-byte chunk c of tile row r is c ^ kv_swz(r), a
+// permutation of (r >> 1) & 7 (rows r and r + 16 share the key).  LDS serves
+// 256 bytes (64 banks) per cycle and a 128-byte row covers half of them, so
+// even and odd rows fall in different halves: 16 consecutive rows read at one
+// logical chunk (K fragments) then hit 16 distinct bank groups, and the four
+// rows r0 + [0, 4) that half a wave's transposed V reads cover (chunks
+// 4 db + [0, 4) of each) do too, since rows r0 and r0 + 2 differ in the
+// key's bit 2.
+__device__ __forceinline__ int kv_swz(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
 
 // LDS byte offset of element (row, col) of a 64 x 64 bf16 tile.
 __device__ __forceinline__ int kv_off(int row, int col) {
@@ -193,9 +199,10 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
   // V^T fragments through transposed reads (see lds_read_tr): lane group
   // g = lane / 16 covers dims 16 * (g % 2) + [0, 16) of a 32-dim block and
   // keys 4 * (g / 2) + [0, 4) of an 8-key half step.  The swizzle key of a
-  // row, (row >> 1) & 7, does not see the 32-row block jb or the 16-row step
-  // u, so those enter as constants (folded into the LDS instructions'
-  // offset fields): koff[st] + 4096 jb, voff[db][hl] + 4096 jb + 2048 u.
+  // row, a function of (row >> 1) & 7, does not see the 32-row block jb or
+  // the 16-row step u, so those enter as constants (folded into the LDS
+  // instructions' offset fields): koff[st] + 4096 jb, voff[db][hl] + 4096 jb
+  // + 2048 u.
   int koff[4], voff[2][2];
   {
     const int tq = lane & 3, tk = (lane >> 2) & 3, tg = lane >> 4;
