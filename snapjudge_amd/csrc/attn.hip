@@ -383,7 +383,8 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
   float l_tot;
   if constexpr (PRE) {
     // First pass without the running max: p = 2^s straight from the MFMA.
-    // It stands when every live query's weight sum lies in [2^-60, 2^64]:
+    // It stands when every live query's weight sum lies in [2^-60, 2^64]
+    // (raised below when the last tile ran past the keys):
     // then no weight, sum or O entry overflowed, and a weight that flushed
     // to zero (below 2^-126) is under 2^-53 of the largest one (>= 2^-60 /
     // 8192), so its loss is far below the bf16 rounding of the weights.
@@ -392,6 +393,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     int* redo = reinterpret_cast<int*>(smem + kNS * kStage);
     if (tid == 0) *redo = 0;  // ordered before other waves' writes by pass 1's barriers
     l_tot = pass(std::true_type{});
+    float l_min = 0x1p-60f;
     if (a.window == 0 && ntiles > 0) {  // uniform
       // the keys at or past klen in the last tile (none before a half item's
       // middle), each counted once with
@@ -400,10 +402,18 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
       // rr / 8 lie past the end)
       auto n_out = [](int rr) { return rr <= 0 ? 32 : rr >= 60 ? 0 : 4 * (7 - (rr >> 3)) + max(0, 4 - (rr & 7)); };
       const int rr = klen - (klo + (ntiles - 1) * kKey);
-      l_tot -= static_cast<float>(n_out(rr) + n_out(rr - 4));
+      const float units = static_cast<float>(n_out(rr) + n_out(rr - 4));
+      l_tot -= units;
+      // While those units sit in the sums, each of the last tile's adds
+      // rounds by up to 2^-24 of (true sum + units): at most 2^-19 (l + units)
+      // over the lane's adds, the two wave halves and the subtraction.  A
+      // true sum of at least units * 2^-6 keeps that below 2^-13 of it; a
+      // smaller one (every weight of the row tiny) runs again with the max
+      // rule, which masks those keys instead.
+      l_min = fmaxf(l_min, units * 0x1p-6f);
     }
     if (ntiles > 0) {  // uniform
-      const bool bad = wave_active && qi < qlen && qhi > qlo && !(l_tot >= 0x1p-60f && l_tot <= 0x1p64f);
+      const bool bad = wave_active && qi < qlen && qhi > qlo && !(l_tot >= l_min && l_tot <= 0x1p64f);
       if (__any(bad) && lane == 0) *redo = 1;
       __syncthreads();
       if (*redo) l_tot = pass(std::false_type{});

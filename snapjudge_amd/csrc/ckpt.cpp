@@ -45,14 +45,23 @@ struct JVal {
     return nullptr;
   }
   bool has(const std::string& k) const { return get(k) != nullptr; }
-  // the reference's json.value(key, default) for numbers
+  const char* type_name() const {
+    static const char* const names[] = {"null", "boolean", "number", "string", "array", "object"};
+    return names[kind];
+  }
+  // the reference's json.value(key, default) for numbers: the default when the
+  // key is absent; a present key must hold a number (a boolean reads as 0 or
+  // 1), anything else fails as the reference's type error does
   double number(const std::string& k, double dflt) const {
     const JVal* v = get(k);
-    return v && v->kind == NUM ? v->num : dflt;
+    if (!v) return dflt;
+    if (v->kind == BOOL) return v->b ? 1.0 : 0.0;
+    if (v->kind != NUM)
+      fail_arg("config key '" + k + "': type must be number, but is " + v->type_name());
+    return v->num;
   }
   int integer(const std::string& k, int dflt) const {
-    const JVal* v = get(k);
-    return v && v->kind == NUM ? static_cast<int>(v->num) : dflt;
+    return static_cast<int>(number(k, static_cast<double>(dflt)));
   }
 };
 

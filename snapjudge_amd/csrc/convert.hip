@@ -21,19 +21,23 @@ __device__ __forceinline__ float half_bits_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+// Grid-stride loops: the grid is capped (blocks() below), so any element
+// count the launchers accept is covered.
 __global__ void widen_kernel(const uint16_t* src, int src_dtype, float* dst, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint16_t h = src[i];
-  dst[i] = src_dtype == SRC_BF16 ? bf16_to_f32(h) : half_bits_to_f32(h);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint16_t h = src[i];
+    dst[i] = src_dtype == SRC_BF16 ? bf16_to_f32(h) : half_bits_to_f32(h);
+  }
 }
 
 __global__ void narrow_kernel(const void* src, int src_dtype, bf16_t* dst, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float v = src_dtype == SRC_F32 ? static_cast<const float*>(src)[i]
-                                       : half_bits_to_f32(static_cast<const uint16_t*>(src)[i]);
-  dst[i] = f32_to_bf16(v);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float v = src_dtype == SRC_F32 ? static_cast<const float*>(src)[i]
+                                         : half_bits_to_f32(static_cast<const uint16_t*>(src)[i]);
+    dst[i] = f32_to_bf16(v);
+  }
 }
 
 // One workgroup per row: the row's largest magnitude (max is exact in any
@@ -64,7 +68,9 @@ __global__ __launch_bounds__(kQT) void quantize_fp8_kernel(const float* w, int64
     qr[c] = fp8_e4m3_rne_bits(__float_as_uint(row[c] / sc));
 }
 
-unsigned blocks(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
+// 256-thread workgroups for n elements, at most 2^16 of them (the kernels
+// loop over the rest)
+unsigned blocks(int64_t n) { return static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 65536)); }
 
 }  // namespace
 

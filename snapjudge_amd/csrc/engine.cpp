@@ -290,8 +290,10 @@ Engine::Engine(const ModelSource& src, const sjh_options& o) {
 Engine::~Engine() {
   (void)hipSetDevice(dev_);
   if (stream_) (void)hipStreamSynchronize(stream_);
-  for (auto& kv : graphs_)
-    if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+  for (auto& kv : graphs_) {
+    if (kv.second.done) (void)hipEventSynchronize(kv.second.done);
+    drop_graph(kv.second);
+  }
   for (auto& p : prof_pending_) {
     (void)hipEventDestroy(p.a);
     (void)hipEventDestroy(p.b);
@@ -673,8 +675,7 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   ws_.attn_part = n_pairs > 0 ? attn_part_.as<float>() : nullptr;
   ws_.attn_pairs_cap = n_pairs;
   ++ws_gen_;
-  for (auto& kv : graphs_)
-    if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+  for (auto& kv : graphs_) drop_graph(kv.second);  // every launch ended (above)
   graphs_.clear();
 }
 
@@ -1262,7 +1263,10 @@ void Engine::run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, fl
       auto lru = graphs_.begin();
       for (auto jt = graphs_.begin(); jt != graphs_.end(); ++jt)
         if (jt->second.last_use < lru->second.last_use) lru = jt;
-      if (lru->second.exec) (void)hipGraphExecDestroy(lru->second.exec);
+      // its last launch may still be queued (calls return before their work
+      // ends): the executable graph is destroyed only after that launch
+      if (lru->second.done) hip_check(hipEventSynchronize(lru->second.done), "wait for an evicted graph");
+      drop_graph(lru->second);
       graphs_.erase(lru);
     }
     hipGraph_t graph = nullptr;
@@ -1279,6 +1283,11 @@ void Engine::run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, fl
     hipError_t e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     hip_check(e, "graph instantiate");
+    e = hipEventCreateWithFlags(&g.done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      drop_graph(g);
+      hip_check(e, "graph event");
+    }
     it = graphs_.emplace(key, g).first;
     ++n_captures_;
   } else {
@@ -1286,6 +1295,14 @@ void Engine::run_device_maybe_graph(const BatchPlan& p, const int32_t* d_ids, fl
   }
   it->second.last_use = ++graph_clock_;
   hip_check(hipGraphLaunch(it->second.exec, st), "graph launch");
+  hip_check(hipEventRecord(it->second.done, st), "record graph launch");
+}
+
+void Engine::drop_graph(Graph& g) {
+  if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  if (g.done) (void)hipEventDestroy(g.done);
+  g.exec = nullptr;
+  g.done = nullptr;
 }
 
 // ------------------------------------------------------------------ entries --

@@ -153,8 +153,10 @@ class Engine {
   };
   struct Graph {
     hipGraphExec_t exec = nullptr;
-    uint64_t last_use = 0;  // LRU eviction
+    hipEvent_t done = nullptr;  // recorded after each launch: eviction waits on it
+    uint64_t last_use = 0;      // LRU eviction
   };
+  void drop_graph(Graph& g);
   static constexpr size_t kMaxGraphs = 32;
 
   void stage_weights(const ModelSource& s);

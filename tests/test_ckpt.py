@@ -70,11 +70,19 @@ def test_well_formed_checkpoints_reach_device_selection(tmp_path):
     ("fp8_without_scale", "missing tensor encoder.layers.0.attn.Wo.weight_scale"),
     ("fp8_elsewhere", "unsupported dtype F8_E4M3 for type_emb.weight"),
     ("bad_lora", "lora_A.weight"),
+    # a number written as a string: the reference's json.value throws a type
+    # error rather than loading the default
+    ("string_layers", "config key 'num_hidden_layers': type must be number, but is string"),
+    ("null_eps", "config key 'norm_eps': type must be number, but is null"),
 ])
 def test_malformed_decision_checkpoints(tmp_path, case, match):
     rl, enc, w = small_decision(tmp_path)
     d = tmp_path / "ck"
     t = dict(w)
+    if case == "string_layers":
+        enc = dict(enc, num_hidden_layers="2")
+    if case == "null_eps":
+        enc = dict(enc, norm_eps=None)
     if case == "missing_head_layers":
         rl = {k: v for k, v in rl.items() if k != "head_layers"}
     if case == "missing_prefix":

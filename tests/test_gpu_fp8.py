@@ -51,9 +51,14 @@ def test_device_decodes_every_code():
 
 
 # (23000, 768, 64): 270 tiles on 256 workgroups, so the last round runs as
-# half-row units
+# half-row units.  M = 20445 is the token count of the bench's config-5 batch,
+# with its QKV (3072 x 1024), Wi (5248 x 1024) and Wo2 (1024 x 2624) weights:
+# several rounds of persistent tiles, the fp8 W ring carried across tile
+# boundaries
 @pytest.mark.parametrize("M,N,K,act,bias", [(1000, 3072, 1024, 0, False), (257, 1024, 2624, 1, True),
-                                            (4500, 256, 64, 2, True), (23000, 768, 64, 1, True)])
+                                            (4500, 256, 64, 2, True), (23000, 768, 64, 1, True),
+                                            (20445, 3072, 1024, 0, False), (20445, 5248, 1024, 0, False),
+                                            (20445, 1024, 2624, 0, True)])
 def test_gemm_fp8w_vs_dequantized_fp32(M, N, K, act, bias):
     rng = np.random.default_rng(M)
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)

@@ -203,7 +203,8 @@ def test_attention_reference_layout(orc, dtype, Dh, window):
     assert float(np.abs(got - want).max()) <= tol
 
 
-@pytest.mark.parametrize("case", ["plain", "window", "large", "negative", "long", "moderate", "mixed"])
+@pytest.mark.parametrize("case", ["plain", "window", "large", "negative", "long", "moderate", "mixed",
+                                  "neg20", "neg30"])
 def test_attention_log2_scaled_queries(orc, case):
     # the encoder's layout: q pre-multiplied by scale * log2(e) before its bf16
     # rounding.  The kernel first runs an item without a softmax offset and
@@ -212,7 +213,11 @@ def test_attention_log2_scaled_queries(orc, case):
     # range and take the second pass; "negative" ones (all below -64) fall
     # under it; "moderate" ones (up to ~45) stay in it; "mixed" has a few
     # all-negative query rows in each workgroup, which sends the whole
-    # workgroup to the second pass; "long" rows cross many key tiles
+    # workgroup to the second pass; "long" rows cross many key tiles.
+    # "neg20" / "neg30": every logit near -20 / -30 (log2 units) with key
+    # counts 150 and 71 (the last tile runs past the keys, whose unit weights
+    # would swamp sums of ~1e-4 and ~1e-7), V offset by 1 so that a
+    # mis-normalised row shows at full size
     print(f"attn log2 {case}", flush=True)
     B, L, H, Dh = 3, 1100 if case == "long" else 150, 2, 64
     lens = [L, 71, 1] if case != "long" else [L, 700, 64]
@@ -228,6 +233,11 @@ def test_attention_log2_scaled_queries(orc, case):
     if case == "mixed":
         qkv[:, :40, 0, :, -1] = -40.0
         qkv[:, :, 1, :, -1] = 10.0
+    if case in ("neg20", "neg30"):
+        c0 = (1.0 / math.sqrt(Dh)) * math.log2(math.e)
+        qkv[:, :, 0, :, -1] = bf16_round(np.float32(-float(case[3:]) / (10.0 * c0)))
+        qkv[:, :, 1, :, -1] = 10.0
+        qkv[:, :, 2] += 1.0
     window = 40 if case == "window" else 0
     c = (1.0 / math.sqrt(Dh)) * math.log2(math.e)
     pre = qkv.copy()

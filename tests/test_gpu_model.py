@@ -324,6 +324,47 @@ def test_graph_replay_serves_a_shape_bucket():
     g_off.close()
 
 
+def test_graph_cache_eviction_waits_for_queued_launches():
+    # More graphs than the cache holds (32), issued back to back with no host
+    # synchronization: every capture past the 32nd evicts the least recently
+    # used graph while its launch may still be queued.  Each output buffer is
+    # its own graph key (plus four shape buckets), and every result equals the
+    # launch-by-launch model's, bit for bit; a second round recaptures evicted
+    # graphs.
+    import torch
+
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg2"], num_hidden_layers=2), seed=47)
+    cfg = synth.flat_cfg(rl, enc)
+    D, V = cfg["hidden_size"], cfg["vocab_size"]
+    g_on = sj.Model(w, cfg, precision=BF16, use_graphs=True)
+    g_off = sj.Model(w, cfg, precision=BF16, use_graphs=False)
+    lens = [1500, 900, 400, 130]  # four buckets; the first call sizes the workspace
+    ids = torch.from_numpy(np.random.default_rng(48).integers(0, V, size=max(lens)).astype(np.int32)).cuda()
+    want = {}
+    for n in lens:
+        out = torch.empty((n, D), dtype=torch.float32, device="cuda")
+        g_off.encode_device(ids.data_ptr(), np.array([n], np.int32), out.data_ptr())
+        torch.cuda.synchronize()
+        want[n] = out.cpu().numpy()
+    calls = [lens[i % 4] for i in range(40)]
+    outs = [torch.full((n, D), float("nan"), dtype=torch.float32, device="cuda") for n in calls]
+    torch.cuda.synchronize()
+    for rnd in range(2):
+        order = range(40) if rnd == 0 else range(12)
+        for i in order:
+            g_on.encode_device(ids.data_ptr(), np.array([calls[i]], np.int32), outs[i].data_ptr())
+        torch.cuda.synchronize()
+        gs = g_on.graph_stats()
+        print(f"round {rnd}: graphs {gs}", flush=True)
+        for i in order:
+            assert np.array_equal(outs[i].cpu().numpy(), want[calls[i]]), f"call {i} n={calls[i]}"
+            outs[i].fill_(float("nan"))
+        assert gs["cached"] == 32
+    assert gs["captures"] == 52 and gs["replays"] == 0
+    g_on.close()
+    g_off.close()
+
+
 def test_calls_on_two_streams_and_forward_are_ordered():
     # encode_device calls on two streams and a forward() on the model's own
     # stream share one workspace: each waits for the previous call.  Issued

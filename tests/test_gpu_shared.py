@@ -100,7 +100,10 @@ def test_shared_sj_model(orc, tmp_path):
 def test_shared_cfg5_widths_match_forward(prec):
     # config 5's widths (D 1024, 16 heads, F 2624, a 2-layer head) at 2
     # encoder layers: 32 sequences x 8 questions, against forward on the
-    # 256-row expanded batch
+    # 256-row expanded batch.  Both take the persistent GEMMs (T >= 4096) and
+    # every kernel's result for a row is independent of the other rows, so
+    # the two agree bit for bit.  (The reference's forward on the bench's
+    # config-5 decision step is checked in tests/test_gpu_bench_batches.py.)
     p = dict(synth.PRESETS["cfg5"])
     p.update(num_hidden_layers=2, max_position_embeddings=1024)
     rl, enc, w = synth.make_model(**p, head_layers=2, n_act=3, seed=61)
@@ -117,7 +120,7 @@ def test_shared_cfg5_widths_match_forward(prec):
     aerr = float(np.abs(act - eact).max())
     print(f"  logits {derr:.3g} act {aerr:.3g}", flush=True)
     assert np.all(lg[~live] == np.float32(-1e4))
-    assert aerr <= 5e-3 and derr <= 5e-2
+    assert derr == 0.0 and aerr == 0.0
     m.close()
 
 
