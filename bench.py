@@ -235,13 +235,10 @@ def encoder_leg(sj, torch, model, ids, lens, D, steps, warmup, stream):
     return elapsed * 1e3 / steps, T * steps / elapsed, prof
 
 
-QTYPE_MARKERS = {0: (4, 16), 1: (5, 5), 2: (2, 2)}  # choice K in [4, 16], score 5, noul 2
-
-
 def decision_leg(model, ids, mask, lens, n_q, steps, seed=3):
     """Config 5's decision step: each of the U sequences carries n_q typed
     questions (qtype uniform over choice / score / noul, src/common.cpp:12-13,
-    with the marker counts above), U * n_q rows through forward_shared: the
+    with synth.QTYPE_MARKERS markers), U * n_q rows through forward_shared: the
     encoder on the U sequences, the head layers once per distinct (sequence,
     qtype) pair, the scorer and act head per row.  Host arrays in, logits and
     act out, as DecisionModel::forward's interface, so the time includes the
@@ -249,13 +246,8 @@ def decision_leg(model, ids, mask, lens, n_q, steps, seed=3):
     the U * n_q-row expansion (every row encoded and run through the head)."""
     from snapjudge_amd import synth
 
-    rng = np.random.default_rng(seed)
     U = len(lens)
-    row_seq = np.repeat(np.arange(U), n_q).astype(np.int32)
-    qt = rng.integers(0, 3, size=len(row_seq))
-    kinds = [(int(t), int(rng.integers(QTYPE_MARKERS[int(t)][0], QTYPE_MARKERS[int(t)][1] + 1)))
-             for t in qt]
-    mp, mm, qt = synth.make_markers(lens[row_seq], 16, kinds, seed=seed)
+    row_seq, mp, mm, qt = synth.make_questions(lens, n_q, seed=seed)
     pairs = len({(int(u), int(t)) for u, t in zip(row_seq, qt)})
 
     def timed(fn, n):

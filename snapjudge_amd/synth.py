@@ -329,3 +329,24 @@ def make_markers(lens, K: int, kinds, seed: int = 0):
         mm[b, :len(pos)] = 1
         qt[b] = qtype
     return mp, mm, qt
+
+
+# marker counts per qtype (src/common.cpp:12-13): choice K in [4, 16], score
+# on a 1-5 scale, noul yes/no
+QTYPE_MARKERS = {0: (4, 16), 1: (5, 5), 2: (2, 2)}
+
+
+def make_questions(lens, n_q: int, seed: int = 3, K: int = 16):
+    """Config 5's typed questions: every sequence carries n_q questions with a
+    uniform qtype (choice / score / noul) and QTYPE_MARKERS markers each.
+    Returns (row_seq [U*n_q] int32, marker_pos [U*n_q, K], marker_mask, qtype):
+    the rows of the reference's forward are the sequences repeated n_q times
+    (one qtype per row, src/model.cpp:410-416)."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens)
+    row_seq = np.repeat(np.arange(len(lens)), n_q).astype(np.int32)
+    qt = rng.integers(0, 3, size=len(row_seq))
+    kinds = [(int(t), int(rng.integers(QTYPE_MARKERS[int(t)][0], QTYPE_MARKERS[int(t)][1] + 1)))
+             for t in qt]
+    mp, mm, qt = make_markers(lens[row_seq], K, kinds, seed=seed)
+    return row_seq, mp, mm, qt

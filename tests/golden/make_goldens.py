@@ -16,6 +16,19 @@ are committed, never weights.
                      bench's batch): the shortest and the longest row, each run
                      alone through all 22 layers (rows are independent,
                      src/tensor.cpp:179-185), hidden states at sampled positions
+  cfg3_b64s512.npz   BASELINE config 3 (the same 22-layer encoder, weights seed
+                     0, batch 64 x seq 512, lengths U[64, 512] seed 1: the
+                     bench's batch): the shortest, the median and the longest
+                     row, each run alone through all 22 layers, hidden states at
+                     sampled positions
+  cfg5_b32s1024.npz  BASELINE config 5 (28 layers, D=1024, fp8 weights seed 0,
+                     batch 32 x seq 1024, lengths U[256, 1024] seed 1, the
+                     bench's 8 typed questions per sequence, seed 3): on the
+                     dequantized twin of the fp8 weights (decode(code) * scale,
+                     stored F32), the shortest and the longest row alone through
+                     all 28 layers (hidden states at sampled positions) and
+                     DecisionModel::forward on each of their 8 question rows
+                     (logits, act)
 """
 import os
 import sys
@@ -107,6 +120,103 @@ def cfg4():
              lens=lens, pos_short=cfg4_positions(int(lens[rows[0]])),
              pos_long=cfg4_positions(int(lens[rows[1]])), hidden_short=outs[0],
              hidden_long=outs[1])
+
+
+def _pool_map(fn, jobs, procs):
+    from multiprocessing import get_context
+
+    with get_context("fork").Pool(procs) as pool:
+        return pool.map(fn, jobs)
+
+
+def sampled_positions(n, step):
+    """The first and last 8 positions of a row of length n and every step-th
+    in between."""
+    return np.unique(np.concatenate([np.arange(min(8, n)), np.arange(max(n - 8, 0), n),
+                                     np.arange(8, max(n - 8, 8), step)])).astype(np.int64)
+
+
+def _encode_row(args):
+    d, ids_row, step, tag = args
+    os.environ["SNAPJUDGE_THREADS"] = "1"
+    n = len(ids_row)
+    ref = RefModel(d)
+    t0 = time.time()
+    h = ref.encode(ids_row[None, :], np.ones((1, n), np.int64))[0]
+    print(f"{tag} encode n={n}: {time.time() - t0:.0f} s", flush=True)
+    return h[sampled_positions(n, step)]
+
+
+def _forward_row(args):
+    d, ids_row, mp, mm, qt, tag = args
+    os.environ["SNAPJUDGE_THREADS"] = "1"
+    n = len(ids_row)
+    ref = RefModel(d)
+    t0 = time.time()
+    logits, act = ref.forward(ids_row[None, :], np.ones((1, n), np.int64), mp[None, :],
+                              mm[None, :], np.array([qt], np.int64))
+    print(f"{tag} forward n={n} qtype={qt}: {time.time() - t0:.0f} s", flush=True)
+    return logits[0], act[0]
+
+
+def cfg3():
+    seed = 0
+    p = dict(synth.PRESETS["cfg3"])
+    rl, enc, w = synth.make_model(**p, seed=seed)
+    ids, _, lens = synth.make_batch(64, 512, 64, 512, enc["vocab_size"], seed=1)
+    order = np.argsort(lens, kind="stable")
+    rows = [int(order[0]), int(order[32]), int(order[-1])]
+    step = 13
+    with tempfile.TemporaryDirectory() as d:
+        synth.write_checkpoint(d, rl, enc, w, store=p["store"])
+        del w
+        outs = _pool_map(_encode_row, [(d, ids[b, :lens[b]].copy(), step, "cfg3") for b in rows],
+                         len(rows))
+    out = dict(seed=seed, batch_seed=1, rows=np.array(rows), lens=lens, step=step)
+    for i, b in enumerate(rows):
+        out[f"pos_{i}"] = sampled_positions(int(lens[b]), step)
+        out[f"hidden_{i}"] = outs[i]
+    np.savez(os.path.join(HERE, "cfg3_b64s512.npz"), **out)
+
+
+def cfg5():
+    import snapjudge_amd as sj
+
+    seed, n_q = 0, 8
+    p = dict(synth.PRESETS["cfg5"])
+    rl, enc, w = synth.make_model(**p, seed=seed)
+    wdq = sj.fp8_dequantized(w)
+    del w
+    ids, _, lens = synth.make_batch(32, 1024, 256, 1024, enc["vocab_size"], seed=1)
+    row_seq, mp, mm, qt = synth.make_questions(lens, n_q, seed=3)
+    rows = [int(np.argmin(lens)), int(np.argmax(lens))]
+    step = 29
+    with tempfile.TemporaryDirectory() as d:
+        synth.write_checkpoint(d, rl, enc, wdq, store="F32")
+        del wdq
+        enc_jobs = [(d, ids[b, :lens[b]].copy(), step, "cfg5") for b in rows]
+        q_rows = [r for b in rows for r in np.nonzero(row_seq == b)[0]]
+        fwd_jobs = [(d, ids[row_seq[r], :lens[row_seq[r]]].copy(), mp[r], mm[r], int(qt[r]), "cfg5")
+                    for r in q_rows]
+        # longest jobs first, so the pool's tail is short
+        jobs = [("e", i, j) for i, j in enumerate(enc_jobs)] + \
+               [("f", i, j) for i, j in enumerate(fwd_jobs)]
+        jobs.sort(key=lambda j: -len(j[2][1]))
+        outs = _pool_map(_cfg5_job, jobs, 7)
+    res = {(kind, i): o for (kind, i, _), o in zip(jobs, outs)}
+    out = dict(seed=seed, batch_seed=1, question_seed=3, n_q=n_q, rows=np.array(rows), lens=lens,
+               step=step, q_rows=np.array(q_rows))
+    for i, b in enumerate(rows):
+        out[f"pos_{i}"] = sampled_positions(int(lens[b]), step)
+        out[f"hidden_{i}"] = res[("e", i)]
+    out["logits"] = np.stack([res[("f", i)][0] for i in range(len(fwd_jobs))])
+    out["act"] = np.stack([res[("f", i)][1] for i in range(len(fwd_jobs))])
+    np.savez(os.path.join(HERE, "cfg5_b32s1024.npz"), **out)
+
+
+def _cfg5_job(job):
+    kind, _, args = job
+    return _encode_row(args) if kind == "e" else _forward_row(args)
 
 
 if __name__ == "__main__":
