@@ -464,6 +464,31 @@ void Engine::stage_weights(const ModelSource& s) {
   }
   attn_split_ = max_len_ >= kAttnSplitMinKeys;
   for (const auto& L : layers_) attn_split_ = attn_split_ && L.window == 0;
+  // LayerNorms folded across the residual GEMMs: the consumer constants of
+  // attn_norm over Wqkv and of mlp_norm over Wi (the persistent kernel's
+  // bf16-activation epilogues, D a multiple of 256 up to 1024, head_dim 64)
+  // Switched off: the first GPU run of this path faulted the device, and
+  // its cause has not been found (the kernels' global addresses check out
+  // on the CPU).  The standalone LayerNorms run instead.
+  ln_fold_ = kLnFoldEnabled && act_dt_ == DT_BF16 && !bert && D % kLnBlock == 0 &&
+             D / kLnBlock <= kLnMaxBlocks && Dh_ == 64 && F % 128 == 0;
+  if (ln_fold_) {
+    for (auto& L : layers_) {
+      const int wdt = w8_ ? DT_FP8 : DT_BF16;
+      if (L.has_attn_norm) {
+        L.ln1_c1.alloc(static_cast<size_t>(3 * D) * 16);
+        if (L.attn_norm_b.get()) L.ln1_c2.alloc(static_cast<size_t>(3 * D) * 4);
+        launch_ln_fold_consts(L.wqkv.get(), wdt, L.wqkv_s.as<float>(), static_cast<int>(3 * D), static_cast<int>(D),
+                              L.attn_norm.as<float>(), L.attn_norm_b.as<float>(), L.ln1_c1.as<uint16_t>(),
+                              L.ln1_c2.as<float>(), stream_);
+      }
+      L.ln2_c1.alloc(static_cast<size_t>(wi_rows) * 16);
+      if (L.mlp_norm_b.get()) L.ln2_c2.alloc(static_cast<size_t>(wi_rows) * 4);
+      launch_ln_fold_consts(L.wi.get(), wdt, L.wi_s.as<float>(), static_cast<int>(wi_rows), static_cast<int>(D),
+                            L.mlp_norm.as<float>(), L.mlp_norm_b.as<float>(), L.ln2_c1.as<uint16_t>(),
+                            L.ln2_c2.as<float>(), stream_);
+    }
+  }
 
   if (lora_r_ > 0) {
     lora_a_ = put_f32(s.lora_a, static_cast<int64_t>(lora_r_) * D, "lora_a");
@@ -647,6 +672,8 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   attn_items_.ensure(attn_items_ints(n_items) * 4);
   const int n_pairs = attn_split_ ? attn_split_pairs(nT, nB, H_) : 0;
   if (n_pairs > 0) attn_part_.ensure(static_cast<size_t>(n_pairs) * 2 * kAttnPartFloats * 4);
+  // moments of every 256-row tile the persistent kernel reads, one tile past the last
+  if (ln_fold_) ln_stats_.ensure(((t + 255) / 256 * 256 + 256) * static_cast<size_t>(D / kLnBlock) * 8);
   X_.ensure(t * D * 4);
   Y_.ensure(t * D * as);
   QKV_.ensure(t * 3 * D * as);
@@ -674,6 +701,7 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   ws_.attn_slots_cap = n_items;
   ws_.attn_part = n_pairs > 0 ? attn_part_.as<float>() : nullptr;
   ws_.attn_pairs_cap = n_pairs;
+  ws_.ln_stats = ln_fold_ ? ln_stats_.as<float>() : nullptr;
   ++ws_gen_;
   for (auto& kv : graphs_) drop_graph(kv.second);  // every launch ended (above)
   graphs_.clear();
@@ -930,11 +958,38 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
   final_args.M = T;
   final_args.M_dev = T_dev;
   final_args.D = D;
+  // LayerNorms folded across the residual GEMMs (GemmArgs::ln_y): on the
+  // persistent kernel's batches the Wo and Wo2 epilogues write the next
+  // LayerNorm's bf16 input rows (centred on each 256-column block's mean,
+  // times the norm weight) and the row moments, and the QKV and Wi products
+  // that read them finish the normalisation in their epilogues: no LayerNorm
+  // launch between the residual GEMMs.  The probe arguments stand for every
+  // layer (same shapes, 256-byte aligned buffers).
+  bool fold = false;
+  if (ln_fold_ && w.ln_stats) {
+    GemmArgs q;
+    q.A = Y, q.lda = D, q.W = layers_[0].wqkv.get(), q.ldw = D, q.M = T, q.N = 3 * D, q.K = D;
+    if (w8_) q.w_dtype = DT_FP8, q.w_scale = layers_[0].wqkv_s.as<float>();
+    q.epi = EPI_ROPE, q.out = QKV, q.ldo = 3 * D, q.head_dim = Dh_, q.rope_dim = D, q.rope_rows = max_pos_;
+    q.rope_cos = rope_cos_full_.as<float>(), q.rope_sin = rope_sin_full_.as<float>();
+    GemmArgs o = q;
+    o.A = O, o.W = layers_[0].wo.get(), o.w_scale = layers_[0].wo_s.as<float>(), o.N = D, o.epi = EPI_RESID;
+    o.out = nullptr, o.ldo = 0, o.X = X, o.ldx = D;
+    GemmArgs i2 = q;
+    i2.W = layers_[0].wi.get(), i2.w_scale = layers_[0].wi_s.as<float>(), i2.N = F, i2.epi = EPI_GEGLU, i2.out = G,
+    i2.ldo = F;
+    GemmArgs o2 = o;
+    o2.A = G, o2.lda = F, o2.W = layers_[0].wo2.get(), o2.w_scale = layers_[0].wo2_s.as<float>(), o2.ldw = F,
+    o2.K = F;
+    fold = gemm_takes_ln_fold(q) && gemm_takes_ln_fold(o) && gemm_takes_ln_fold(i2) && gemm_takes_ln_fold(o2);
+  }
   for (int li = 0; li < nlayers_; ++li) {
     const LayerDev& ly = layers_[static_cast<size_t>(li)];
     // layers after the first get their attn_norm from the previous layer's
-    // Wo2 step (resid_gemm_ln)
+    // Wo2 step (resid_gemm_ln, or folded)
     if (li == 0 && ly.has_attn_norm) ln("attn_norm", attn_norm_args(0), st);
+    // this layer's QKV product reads the previous Wo2's folded rows
+    const bool fold_in = fold && li > 0 && ly.has_attn_norm;
     {  // qkv = Y . Wqkv^T with RoPE on q, k (src/model.cpp:355-365); BERT:
        // q|k|v rows with their biases, no RoPE (src/sj_model.cpp:44-52)
       GemmArgs g;
@@ -964,6 +1019,12 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
         g.rope_dim = D;
         g.head_dim = Dh_;
         if (q_pre) g.q_scale = scale * 1.4426950408889634f;
+        if (fold_in) {
+          g.ln_stats_in = w.ln_stats;
+          g.ln_c1 = ly.ln1_c1.as<uint16_t>();
+          g.ln_c2 = ly.ln1_c2.as<float>();
+          g.ln_eps = eps_;
+        }
         gemm("gemm_qkv_rope", g, w, st);
       }
     }
@@ -1028,7 +1089,14 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       a.M = T;
       a.M_dev = T_dev;
       a.D = D;
-      resid_gemm_ln("gemm_wo_resid", g, "mlp_norm", a, w, st);
+      if (fold) {
+        g.ln_y = Y;
+        g.ln_w = ly.mlp_norm.as<float>();
+        g.ln_stats_out = w.ln_stats;
+        gemm("gemm_wo_resid", g, w, st);
+      } else {
+        resid_gemm_ln("gemm_wo_resid", g, "mlp_norm", a, w, st);
+      }
     }
     {  // G = geglu(Y . Wi^T) (src/model.cpp:394); BERT: G = gelu(Y . W1^T + b1)
        // (src/sj_model.cpp:249)
@@ -1053,6 +1121,12 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
         gemm("gemm_w1_gelu", g, w, st);
       } else {
         g.epi = EPI_GEGLU;
+        if (fold) {
+          g.ln_stats_in = w.ln_stats;
+          g.ln_c1 = ly.ln2_c1.as<uint16_t>();
+          g.ln_c2 = ly.ln2_c2.as<float>();
+          g.ln_eps = eps_;
+        }
         gemm("gemm_wi_geglu", g, w, st);
       }
     }
@@ -1072,11 +1146,18 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       g.X = X;
       g.ldx = D;
       g.bias = ly.wo2_b.as<float>();
-      // then the next layer's attn_norm, or the final norm
-      if (li + 1 < nlayers_)
+      // then the next layer's attn_norm (folded into its QKV product), or
+      // the final norm
+      if (li + 1 < nlayers_ && fold && layers_[static_cast<size_t>(li + 1)].has_attn_norm) {
+        g.ln_y = Y;
+        g.ln_w = layers_[static_cast<size_t>(li + 1)].attn_norm.as<float>();
+        g.ln_stats_out = w.ln_stats;
+        gemm("gemm_wo2_resid", g, w, st);
+      } else if (li + 1 < nlayers_) {
         resid_gemm_ln("gemm_wo2_resid", g, "attn_norm", attn_norm_args(li + 1), w, st);
-      else
+      } else {
         resid_gemm_ln("gemm_wo2_resid", g, "final_norm", final_args, w, st);
+      }
     }
   }
   if (lora_r_ > 0) {  // h += (h . A^T) . B^T (src/model.cpp:402-407)

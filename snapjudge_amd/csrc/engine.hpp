@@ -101,6 +101,7 @@ struct Ws {
   int attn_slots_cap = 0;         // its slots
   float* attn_part = nullptr;     // partials of key-split items (AttnArgs::part), or none
   int attn_pairs_cap = 0;         // split items they hold
+  float* ln_stats = nullptr;      // row moments of a folded LayerNorm (GemmArgs::ln_stats_out), or none
 };
 
 class Engine {
@@ -142,6 +143,9 @@ class Engine {
     DevBuf attn_norm, attn_norm_b, wqkv, wqkv_b, wo, wo_b, mlp_norm, mlp_norm_b, wi, wi_b, wo2,
         wo2_b;                         // the biases and norm biases of the BERT family
     DevBuf wqkv_s, wo_s, wi_s, wo2_s;  // per-row scales of fp8 projections
+    // consumer constants of a folded LayerNorm (GemmArgs::ln_c1 / ln_c2):
+    // attn_norm over Wqkv, mlp_norm over Wi
+    DevBuf ln1_c1, ln1_c2, ln2_c1, ln2_c2;
     bool has_attn_norm = false;
     int window = 0, sliding = 0;
   };
@@ -220,6 +224,9 @@ class Engine {
   int n_act_ = 0, head_layers_ = 0, lora_r_ = 0, max_len_ = 0;
   float eps_ = 1e-5f;
   bool attn_split_ = false;  // every layer has full attention and sequences can reach kAttnSplitMinKeys
+  // the encoder's LayerNorms after its residual GEMMs can fold into them and
+  // the next GEMMs (GemmArgs::ln_y) on the persistent kernel's batches
+  bool ln_fold_ = false;
   int arch_ = ARCH_MODERNBERT;  // ModernBERT (DecisionModel) or BERT (SjModel)
   int act_head_ = ACT_MLP;
   int head_ff_ = 0, head_act_ = 2;
@@ -244,6 +251,7 @@ class Engine {
   DevBuf splitk_;  // split-K partial sums for short batches (GemmArgs::partial)
   DevBuf attn_items_;  // attention work list (AttnArgs::items)
   DevBuf attn_part_;   // partials of key-split attention items (AttnArgs::part)
+  DevBuf ln_stats_;    // folded LayerNorm row moments (Ws::ln_stats)
   Ws ws_;          // views of the buffers above
   DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_lg_, tail_ain_, tail_ah_,
       tail_ao_, tail_act_;

@@ -387,6 +387,264 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
   }
 }
 
+// ---- LayerNorm folded across a residual GEMM and the next GEMM -------------
+// (GemmArgs::ln_y / ln_stats_in).  Both sides run in the persistent kernel's
+// direct accumulator layout (lane l holds column l % 32 of each 32x32 block
+// and rows 8 (e / 4) + 4 (l / 32) + e % 4) or, for the consumer, the
+// transposed one (lane l holds row l % 32).
+
+// Reduce-scatter of 16 row sums over the 32 lanes of a wave half (one
+// column each): every stage pairs the lanes that differ in one bit (16, 8, 4,
+// 2), each keeps half of the slots and adds its partner's value for them.
+// Then lanes 2k and 2k + 1 hold the whole sum of slot k (in both).  Float
+// addition is commutative, so every slot's sum is the same function of its
+// 32 values, whichever slot (row) it is.
+__device__ __forceinline__ float rows16_sum(float (&v)[16], int l32) {
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {  // lanes l and l ^ 16: one swap moves both halves
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[p]), __float_as_uint(v[p + 8]), false, false);
+    v[p] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  auto stage = [&](auto c_tag, auto s_tag) {
+    constexpr int C = decltype(c_tag)::value, S = decltype(s_tag)::value;
+    const bool up = (l32 & S) != 0;
+#pragma unroll
+    for (int p = 0; p < C / 2; ++p) {
+      const float lo = v[p], hi = v[p + C / 2];
+      const float keep = up ? hi : lo, send = up ? lo : hi;
+      v[p] = keep + __shfl_xor(send, S, 64);
+    }
+  };
+  stage(std::integral_constant<int, 8>{}, std::integral_constant<int, 8>{});
+  stage(std::integral_constant<int, 4>{}, std::integral_constant<int, 4>{});
+  stage(std::integral_constant<int, 2>{}, std::integral_constant<int, 2>{});
+  return v[0] + __shfl_xor(v[0], 1, 64);
+}
+// The row (within a 32-row block) of the slot that lane l32 of half hb holds
+// after rows16_sum: slot k = l32 / 2 is row 8 (k / 4) + 4 hb + k % 4.
+__device__ __forceinline__ int rows16_row(int l32, int hb) {
+  const int k = l32 >> 1;
+  return 8 * (k >> 2) + 4 * hb + (k & 3);
+}
+
+// Producer: the residual epilogue (X += acc + bias, the same arithmetic as
+// gemm_epilogue's) that also writes the next LayerNorm's input rows and the
+// row moments of this tile's 256 columns.  Two passes over the registers:
+// block means, then squared deviations from them; each reduces over the 64
+// columns of a wave (rows16_sum) and over the WGN waves of the tile through
+// LDS in a fixed order.  Every wave of the workgroup calls it (waves with no
+// rows in a half unit with busy = false): it holds three barriers.
+// red: WGN * BM floats, mu: BM floats of LDS; tid: the thread's index in the
+// workgroup (passed in, so that the kernel need not keep threadIdx.x live
+// through its K loop).
+template <int BM, int BN, int WM, int WN, int TI, int TJ, int WGN>
+__device__ __forceinline__ void resid_ln_epilogue(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int m0,
+                                                  int unit_rows, int tile_n, int wm, int wn, int l32,
+                                                  int hb, int tid, bool busy, float* red, float* mu) {
+  static_assert(BN == kLnBlock, "one LayerNorm block per column tile");
+  const int c0 = tile_n * BN + wn * WN;
+  const int rw = m0 + wm * WM;  // the wave's first row
+  const uint32_t ld4 = static_cast<uint32_t>(g.ldx) * 4u, ld2 = static_cast<uint32_t>(g.ldx) * 2u;
+  char* xw = reinterpret_cast<char*>(g.X + static_cast<int64_t>(rw) * g.ldx + c0);
+  char* yw = reinterpret_cast<char*>(static_cast<bf16_t*>(g.ln_y) + static_cast<int64_t>(rw) * g.ldx + c0);
+  const uint32_t lo4 = 4 * hb * ld4 + l32 * 4, lo2 = 4 * hb * ld2 + l32 * 2;
+  const int rows_in = min(g.M - rw, WM);  // the wave's rows below M (may be <= 0)
+  if (busy) {
+    float bv[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) bv[j] = g.bias ? g.bias[c0 + j * 32 + l32] : 0.f;
+    constexpr int RG = 4;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e0 = 0; e0 < 16; e0 += RG) {
+        float xv[RG][TJ];
+#pragma unroll
+        for (int e = 0; e < RG; ++e) {
+          const int r = i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3) + 4 * hb;
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            xv[e][j] = r < rows_in ? *reinterpret_cast<const float*>(xw + static_cast<uint32_t>((r - 4 * hb) * ld4 + lo4) + j * 128) : 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < RG; ++e) {
+          const int r = i * 32 + 8 * ((e0 + e) >> 2) + ((e0 + e) & 3) + 4 * hb;
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            acc[i][j][e0 + e] = xv[e][j] + (acc[i][j][e0 + e] + bv[j]);
+            if (r < rows_in)
+              *reinterpret_cast<float*>(xw + static_cast<uint32_t>((r - 4 * hb) * ld4 + lo4) + j * 128) = acc[i][j][e0 + e];
+          }
+        }
+      }
+    // pass 1: row sums over the wave's columns
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        v[e] = acc[i][0][e];
+#pragma unroll
+        for (int j = 1; j < TJ; ++j) v[e] += acc[i][j][e];
+      }
+      const float sum = rows16_sum(v, l32);
+      if ((l32 & 1) == 0) red[wn * BM + wm * WM + i * 32 + rows16_row(l32, hb)] = sum;
+    }
+  }
+  __syncthreads();
+  if (tid < BM) {
+    float s = red[tid];
+#pragma unroll
+    for (int w = 1; w < WGN; ++w) s += red[w * BM + tid];
+    mu[tid] = s * (1.0f / BN);
+  }
+  __syncthreads();
+  if (busy) {
+    float lw[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) lw[j] = g.ln_w[c0 + j * 32 + l32];
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const f32x4_t m4 = *reinterpret_cast<const f32x4_t*>(mu + wm * WM + i * 32 + 8 * e4 + 4 * hb);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int e = 4 * e4 + t;
+          const int r = i * 32 + 8 * e4 + t + 4 * hb;
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            acc[i][j][e] -= m4[t];
+            if (r < rows_in)
+              *reinterpret_cast<bf16_t*>(yw + static_cast<uint32_t>((r - 4 * hb) * ld2 + lo2) + j * 64) =
+                  f32_to_bf16(acc[i][j][e] * lw[j]);
+          }
+        }
+      }
+      // pass 2: squared deviations
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        v[e] = acc[i][0][e] * acc[i][0][e];
+#pragma unroll
+        for (int j = 1; j < TJ; ++j) v[e] = __builtin_fmaf(acc[i][j][e], acc[i][j][e], v[e]);
+      }
+      const float ss = rows16_sum(v, l32);
+      if ((l32 & 1) == 0) red[wn * BM + wm * WM + i * 32 + rows16_row(l32, hb)] = ss;
+    }
+  }
+  __syncthreads();
+  if (tid < unit_rows && m0 + tid < g.M) {
+    float m2 = red[tid];
+#pragma unroll
+    for (int w = 1; w < WGN; ++w) m2 += red[w * BM + tid];
+    const int nbn = g.N / kLnBlock;
+    typedef __attribute__((ext_vector_type(2))) float f2_t;
+    *reinterpret_cast<f2_t*>(g.ln_stats_out + (static_cast<int64_t>(m0 + tid) * nbn + tile_n) * 2) =
+        (f2_t){mu[tid], m2};
+  }
+}
+
+// Consumer, part 1 (threads tid < BM of the workgroup, then a barrier by
+// the caller): the unit's per-row LayerNorm values from the producer's block
+// moments (copied to LDS at `stage` when the unit's K loop began), combined
+// in double (src/tensor.cpp:63-71: mean and population variance in double,
+// the inverse std rounded to float).  tab: BM rows of 16 bytes (the bf16
+// deviations d_b = mu_b - mu, zero past the row's blocks: an MFMA operand
+// row), then BM floats r = 1 / sqrt(var + eps).
+__device__ __forceinline__ void ln_fold_table(const GemmArgs& g, const char* stage, char* tab, int tid,
+                                              int BM) {
+  const int nb = g.K / kLnBlock;
+  const float* st = reinterpret_cast<const float*>(stage) + tid * nb * 2;
+  double sum = 0.0;
+#pragma unroll
+  for (int b = 0; b < kLnMaxBlocks; ++b)
+    if (b < nb) sum += st[2 * b];
+  const double mean = sum / nb;
+  double m2 = 0.0;
+#pragma unroll
+  for (int b = 0; b < kLnMaxBlocks; ++b)
+    if (b < nb) {
+      const double d = st[2 * b] - mean;
+      m2 += st[2 * b + 1] + static_cast<double>(kLnBlock) * d * d;
+    }
+  const double var = m2 / (static_cast<double>(kLnBlock) * nb);
+  reinterpret_cast<float*>(tab + 16 * BM)[tid] = static_cast<float>(1.0 / sqrt(var + static_cast<double>(g.ln_eps)));
+  bf16x8_t dv = {};
+#pragma unroll
+  for (int b = 0; b < kLnMaxBlocks; ++b)
+    if (b < nb) dv[b] = static_cast<__bf16>(static_cast<float>(st[2 * b] - mean));
+  *reinterpret_cast<bf16x8_t*>(tab + 16 * tid) = dv;
+}
+
+// Consumer, part 2 (per wave, before its epilogue): acc += d . c1 as one more
+// MFMA per block (the deviations in the K slots of the A side, c1 on the W
+// side, zeros in the upper 8 K slots), then acc *= r of the row, then + c2.
+template <int BM, int BN, int WM, int WN, int TI, int TJ, int EPI, bool SWAP>
+__device__ __forceinline__ void ln_fold_acc(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int tile_n, int wm,
+                                            int wn, int l32, int hb, const char* tab) {
+  const bf16x8_t zero = {};
+  bf16x8_t df[TI], cf[TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+    df[i] = hb == 0 ? *reinterpret_cast<const bf16x8_t*>(tab + 16 * (wm * WM + i * 32 + l32)) : zero;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int64_t wr = mfma_w_row<BN, WN, EPI>(g, tile_n, wn * WN + j * 32 + l32);
+    cf[j] = hb == 0 ? *reinterpret_cast<const bf16x8_t*>(g.ln_c1 + wr * 8) : zero;
+  }
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+      acc[i][j] = SWAP ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[j], df[i], acc[i][j], 0, 0, 0)
+                       : __builtin_amdgcn_mfma_f32_32x32x16_bf16(df[i], cf[j], acc[i][j], 0, 0, 0);
+  const float* tr = reinterpret_cast<const float*>(tab + 16 * BM) + wm * WM;
+  if constexpr (SWAP) {
+    // lane l32 holds row 32 i + l32 and W rows 8 q + 4 hb + t of each block
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      const float r = tr[i * 32 + l32];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] *= r;
+    }
+    if (g.ln_c2) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float c = g.ln_c2[mfma_w_row<BN, WN, EPI>(g, tile_n, wn * WN + j * 32 + 8 * (e >> 2) + 4 * hb + (e & 3))];
+#pragma unroll
+          for (int i = 0; i < TI; ++i) acc[i][j][e] += c;
+        }
+    }
+  } else {
+    // lane l32 holds W row 32 j + l32 and rows 8 (e / 4) + 4 hb + e % 4
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const f32x4_t r4 = *reinterpret_cast<const f32x4_t*>(tr + i * 32 + 8 * e4 + 4 * hb);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[i][j][4 * e4 + t] *= r4[t];
+      }
+    if (g.ln_c2) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const float c = g.ln_c2[mfma_w_row<BN, WN, EPI>(g, tile_n, wn * WN + j * 32 + l32)];
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] += c;
+      }
+    }
+  }
+}
+
 // ---- direct-to-LDS variant -------------------------------------------------
 // Tiles move from HBM to LDS with global_load_lds_dwordx4 (no VGPR staging):
 // lane l of an instruction writes its 16 bytes at LDS address base + 16*l, so
@@ -819,7 +1077,8 @@ constexpr int pers_waves_per_simd() {
   return std::max(1, std::min(4, pers_occupancy<BM, BN, WGM, WGN, NS, BK, W8>() * WGM * WGN / 4));
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8, int EPI, typename OutT>
+// LNF: 0, or a folded LayerNorm's consumer (1) or producer (2, EPI_RESID)
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8, int EPI, typename OutT, int LNF>
 __global__ __launch_bounds__(64 * WGM * WGN, (pers_waves_per_simd<BM, BN, WGM, WGN, NS, BK, W8>()))
 void gemm_bf16_pers_kernel(GemmArgs g0) {
   using TT = PTile<BM, BN, WGM, WGN, NS, BK, W8>;
@@ -1015,6 +1274,8 @@ void gemm_bf16_pers_kernel(GemmArgs g0) {
       }
     }
     const int m0 = tm * BM + (th < 0 ? 0 : (BM / 2) * th);
+    static_assert(LNF == 0 || (LNF == 1 && EPI != EPI_RESID) || (LNF == 2 && EPI == EPI_RESID),
+                  "folded LayerNorm roles");
     // RoPE units: positions of the unit's 256 rows to LDS (waves 0-3, 64 rows
     // each), copied during the first K step and read at the unit's end
     int* pos_lds = reinterpret_cast<int*>(dsmem + NS * TT::STAGE_BYTES);
@@ -1024,6 +1285,21 @@ void gemm_bf16_pers_kernel(GemmArgs g0) {
           __builtin_amdgcn_global_load_lds(g.pos + min(m0 + 64 * wave_s + lane_id_here(), g.M - 1),
                                            (__attribute__((address_space(3))) void*)(pos_lds + 64 * wave_s),
                                            4, 0, 0);
+      }
+    };
+    // a folded LayerNorm's LDS, past the ring and the RoPE positions: the
+    // consumer's copy of the unit's row moments and its row table, or the
+    // producer's reduction rows
+    char* fold_lds = dsmem + NS * TT::STAGE_BYTES + 1024;
+    char* fold_tab = fold_lds + BM * kLnMaxBlocks * 8;
+    // consumer: the moments of the unit's BM rows (contiguous; the buffer
+    // holds rows past M), copied during the first K step
+    auto copy_stats = [&]() {
+      if constexpr (LNF == 1) {
+        const int chunks = BM * (g.K / kLnBlock) * 8 / 1024;
+        const char* src = reinterpret_cast<const char*>(g.ln_stats_in) +
+                          static_cast<int64_t>(m0) * (g.K / kLnBlock) * 8 + lane_id_here() * 16;
+        for (int c = wave_s; c < chunks; c += NW) load_lds16(src + c * 1024, fold_lds + c * 1024);
       }
     };
     // uniform: the unit's tile has rotated columns
@@ -1043,7 +1319,10 @@ void gemm_bf16_pers_kernel(GemmArgs g0) {
                             lane_id_here());
         else if (q + NS - 1 < total)
           issue_next((q + NS - 1 + so) % NS);
-        if (kt == 0) copy_pos();
+        if (kt == 0) {
+          copy_pos();
+          copy_stats();
+        }
         if constexpr (!decltype(busy)::value) continue;
         const char* sb = dsmem + ((q + so) % NS) * TT::STAGE_BYTES;
         // operand reads of step 0 go out first; the previous stage's last K
@@ -1106,13 +1385,39 @@ void gemm_bf16_pers_kernel(GemmArgs g0) {
         }
       }
     };
+    auto ln_table = [&]() {  // every wave takes part (barriers)
+      if constexpr (LNF == 1) {
+        // this wave's copy has landed: the loads issued after it (at least
+        // NS - 1 stages when the unit has more K steps than the ring) may
+        // still be in flight, older ones not
+        if (nk >= NS + 1)
+          wait_vmcnt<G * (NS - 1)>();
+        else
+          wait_vmcnt<0>();
+        __syncthreads();
+        const int tid_e = wave_s * 64 + lane_id_here();
+        if (tid_e < BM) ln_fold_table(g, fold_lds, fold_tab, tid_e, BM);
+        __syncthreads();
+      }
+    };
+    const int unit_rows = th < 0 ? BM : BM / 2;
     if (idle) {
       kloop(std::false_type{});
       stage_tables();
+      ln_table();
+      if constexpr (LNF == 2) {
+        {  // its barriers
+          const int lane_e = lane_id_here();
+          resid_ln_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, WGN>(
+              g, acc, m0, unit_rows, tn, wm_s, wave_s % WGN, lane_e & 31, lane_e >> 5, wave_s * 64 + lane_e, false,
+              reinterpret_cast<float*>(fold_lds), reinterpret_cast<float*>(fold_lds) + WGN * BM);
+        }
+      }
       continue;
     }
     kloop(std::true_type{});
     stage_tables();
+    ln_table();
     // the epilogue's lane and wave indices, recomputed after the K loop
     // rather than held through it
     const int lane_e = lane_id_here(), l32e = lane_e & 31, hbe = lane_e >> 5;
@@ -1147,6 +1452,14 @@ void gemm_bf16_pers_kernel(GemmArgs g0) {
         }
       }
     }
+    if constexpr (LNF == 1)  // A holds folded LayerNorm rows
+      ln_fold_acc<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, kSwap>(g, acc, tn, wme, wne, l32e, hbe, fold_tab);
+    if constexpr (LNF == 2) {  // the next LayerNorm's input rows and moments too
+      resid_ln_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, WGN>(
+          g, acc, m0, unit_rows, tn, wme, wne, l32e, hbe, wave_s * 64 + lane_e, true, reinterpret_cast<float*>(fold_lds),
+          reinterpret_cast<float*>(fold_lds) + WGN * BM);
+      continue;
+    }
     if constexpr (kSwap)
       pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wme, wne, l32e, hbe);
     else
@@ -1167,11 +1480,15 @@ int num_cus() {
   return n;
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8, int EPI, typename OutT>
+template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8, int EPI, typename OutT, int LNF>
 void launch_pers_kernel(const GemmArgs& g, hipStream_t st) {
-  // (+ 1 KB of row positions for the RoPE epilogue)
-  constexpr int lds = NS * PTile<BM, BN, WGM, WGN, NS, BK, W8>::STAGE_BYTES + (EPI == EPI_ROPE ? 1024 : 0);
-  auto kern = gemm_bf16_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI, OutT>;
+  // (+ 1 KB of row positions for the RoPE epilogue, + a folded LayerNorm's
+  // tables: the consumer's moments copy (8 bytes per row and block) and row
+  // table (16 + 4 bytes per row), or the producer's WGN + 1 floats per row)
+  constexpr int fold = LNF == 1 ? BM * (kLnMaxBlocks * 8 + 20) : LNF == 2 ? 4 * (WGN + 1) * BM : 0;
+  constexpr int lds = NS * PTile<BM, BN, WGM, WGN, NS, BK, W8>::STAGE_BYTES + 1024 + fold;
+  static_assert(lds <= 160 * 1024, "LDS");
+  auto kern = gemm_bf16_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI, OutT, LNF>;
   static bool attr_set = false;
   if (!attr_set) {
     hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1190,21 +1507,28 @@ void launch_pers_kernel(const GemmArgs& g, hipStream_t st) {
 template <int BM, int BN, int WGM, int WGN, int NS, int BK, bool W8>
 void launch_pers(const GemmArgs& g, hipStream_t st) {
   const bool bf = g.out_dtype == DT_BF16;
+  // a folded LayerNorm's consumer: bf16 outputs of the QKV and GEGLU products
+  const bool lni = g.ln_stats_in != nullptr;
+  require(!lni || (bf && (g.epi == EPI_ROPE || g.epi == EPI_GEGLU)),
+          "gemm: a folded LayerNorm's consumer is a bf16 RoPE or GEGLU product");
   switch (g.epi) {
     case EPI_STORE:
-      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_STORE, bf16_t>(g, st)
-         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_STORE, float>(g, st);
+      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_STORE, bf16_t, 0>(g, st)
+         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_STORE, float, 0>(g, st);
       break;
     case EPI_RESID:
-      launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_RESID, float>(g, st);
+      g.ln_y ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_RESID, float, 2>(g, st)
+             : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_RESID, float, 0>(g, st);
       break;
     case EPI_ROPE:
-      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_ROPE, bf16_t>(g, st)
-         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_ROPE, float>(g, st);
+      lni  ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_ROPE, bf16_t, 1>(g, st)
+      : bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_ROPE, bf16_t, 0>(g, st)
+           : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_ROPE, float, 0>(g, st);
       break;
     default:
-      bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_GEGLU, bf16_t>(g, st)
-         : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_GEGLU, float>(g, st);
+      lni  ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_GEGLU, bf16_t, 1>(g, st)
+      : bf ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_GEGLU, bf16_t, 0>(g, st)
+           : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_GEGLU, float, 0>(g, st);
       break;
   }
 }
@@ -1513,6 +1837,15 @@ bool mfma_ok(const GemmArgs& g) {
          (g.epi != EPI_ROPE || g.head_dim == 64) && (g.epi != EPI_GEGLU || g.N % 64 == 0);
 }
 
+bool gemm_takes_ln_fold(const GemmArgs& g) {
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || !g.A || !g.W) return false;
+  if (g.w_dtype == DT_FP8)  // the persistent kernel always (launch_gemm's checks)
+    return g.in_dtype == DT_BF16 && g.w_scale && aligned16(g.w_scale) && g.K % 64 == 0 &&
+           g.lda % 8 == 0 && g.ldw % 16 == 0 && aligned16(g.A) && aligned16(g.W) && pers_ok(g) &&
+           (g.epi != EPI_ROPE || g.head_dim == 64);
+  return g.w_dtype == DT_BF16 && mfma_ok(g) && g.M >= 4096 && pers_ok(g);  // launch_mfma's first choice
+}
+
 int launch_gemm_resid_partials(const GemmArgs& g0, hipStream_t st) {
   if (g0.epi != EPI_RESID || g0.M <= 0 || g0.M > SJH_SPLITK_MAX_M || g0.N <= 0 || g0.K <= 0 || !g0.partial ||
       !g0.A || !g0.W || !g0.X || g0.lda < g0.K || g0.ldw < g0.K || g0.ldx < g0.N || !mfma_ok(g0))
@@ -1546,6 +1879,17 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
       break;
     default:
       fail("gemm: unknown epilogue");
+  }
+  if (g.ln_y || g.ln_stats_in) {
+    require(gemm_takes_ln_fold(g),
+            "gemm: a folded LayerNorm needs the persistent kernel (bf16 activations and M >= 4096, or fp8 weights)");
+    require(!g.ln_y || (g.epi == EPI_RESID && g.N % kLnBlock == 0 && g.ln_w && g.ln_stats_out &&
+                        aligned16(g.ln_y) && aligned16(g.ln_stats_out) && g.ldx % 8 == 0),
+            "gemm: a folded LayerNorm's producer is a residual GEMM with N % 256 == 0, weights, moments "
+            "and 16-byte aligned rows");
+    require(!g.ln_stats_in || (g.K % kLnBlock == 0 && g.K / kLnBlock <= kLnMaxBlocks && g.ln_c1 &&
+                               aligned16(g.ln_c1) && aligned16(g.ln_stats_in) && g.ln_eps > 0.f),
+            "gemm: a folded LayerNorm's consumer needs K % 256 == 0, K <= 1024, c1 rows and moments");
   }
   if (g.w_dtype == DT_FP8) {
     // fp8 weights: the persistent kernel only (16-byte fp8 rows chunks)

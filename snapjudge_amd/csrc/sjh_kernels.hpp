@@ -64,8 +64,45 @@ struct GemmArgs {
   int k_chunk = 0;  // K steps (of the MFMA K depth) per split
   int n_w = 0;      // rows of W (= N, or 2F for GEGLU)
   int part_rows = 0;  // the launch's M: split s of row m sits at partial[(s * part_rows + m) * n_w]
+  // A LayerNorm folded across a residual GEMM and the GEMM that reads its
+  // rows next (persistent bf16-activation path only; the launcher rejects
+  // anything else).  Rows are cut into blocks of kLnBlock columns.
+  //  Producer (EPI_RESID with ln_y, N % kLnBlock == 0): besides X += acc
+  //    (+ bias) it writes ln_y[m][c] = bf16((x[m][c] - mu_b) * ln_w[c]) (row
+  //    stride ldx), mu_b the mean of row m over its block b = c / kLnBlock,
+  //    and ln_stats_out[(m * N / kLnBlock + b) * 2 + {0, 1}] = {mu_b, M2_b},
+  //    M2_b the block's sum of squared deviations from mu_b.
+  //  Consumer (ln_stats_in, K % kLnBlock == 0, K <= kLnMaxBlocks * kLnBlock,
+  //    a bf16 RoPE or GEGLU product; ln_stats_in holds the moments of at
+  //    least round_up(M, 256) + 256 rows, read in whole 256-row tiles): A holds such rows.  The
+  //    epilogue first takes acc to r_m * (acc + sum_b d_mb * c1[n][b]) + c2[n]
+  //    with d_mb = mu_b - mu_m and r_m = 1 / sqrt(var_m + eps) from the row's
+  //    combined moments (src/tensor.cpp:54-79), c1[n][b] = sum over block b of
+  //    ln_w[k] W[n][k] and c2 = W . ln_b: that is LN(x) . W^T, with x rounded
+  //    to bf16 after centring on its block's mean.
+  void* ln_y = nullptr;                 // bf16
+  const float* ln_w = nullptr;          // [N]
+  float* ln_stats_out = nullptr;
+  const float* ln_stats_in = nullptr;
+  const uint16_t* ln_c1 = nullptr;      // bf16 [n_w][8], blocks past K / kLnBlock zero
+  const float* ln_c2 = nullptr;         // [n_w] or null (an unbiased norm)
+  float ln_eps = 1e-5f;
 };
+constexpr int kLnBlock = 256;
+// The engine does not take the folded path (see Engine::stage_weights).
+constexpr bool kLnFoldEnabled = false;
+constexpr int kLnMaxBlocks = 4;  // D <= 1024 (c1 rows hold 8 bf16, blocks past 4 zero)
 void launch_gemm(const GemmArgs& g, hipStream_t st);
+// Whether a GEMM of these arguments takes the persistent kernel, the only
+// one that can produce or consume a folded LayerNorm.
+bool gemm_takes_ln_fold(const GemmArgs& g);
+// The consumer constants of a folded LayerNorm for weights W [n_w, K] (bf16,
+// or fp8 codes with per-row scales w_scale: the effective rows code * scale):
+// c1[n][b] = sum over block b of ln_w[k] W[n][k] (bf16, [n_w][8]) and, with
+// ln_b, c2[n] = sum_k ln_b[k] W[n][k] (fp32), both summed in double.
+void launch_ln_fold_consts(const void* W, int w_dtype, const float* w_scale, int n_w, int K,
+                           const float* ln_w, const float* ln_b, uint16_t* c1, float* c2,
+                           hipStream_t st);
 // Short batches (M <= 256) of a residual GEMM (EPI_RESID, bf16 MFMA path):
 // launches only the split-K product into g.partial and returns the number of
 // splits S >= 2; the caller then adds the splits with the layer norm that

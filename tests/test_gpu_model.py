@@ -199,6 +199,47 @@ def test_cfg3_shape_sampled_rows_and_batch_invariance(orc):
     m.close()
 
 
+@pytest.mark.skip(reason="the folded LayerNorm path is switched off: its first GPU run faulted the "
+                         "device and the cause is not found yet")
+@pytest.mark.parametrize("offset", ["row", "block"])
+def test_folded_layer_norm_under_large_row_offsets(orc, offset):
+    # On the persistent kernel's batches (T >= 4096) the LayerNorms after the
+    # residual GEMMs are folded: the residual epilogue rounds x to bf16 after
+    # centring it on its 256-column block's mean, and the next GEMM finishes
+    # the normalisation.  A rank-1 term added to every layer's Wo2 puts a
+    # large offset on each row of the residual stream: the same for every
+    # column ("row", ~100x the spread; LN removes it) or a different one per
+    # 256-column block ("block"; the folded correction carries it).  Sampled
+    # rows against the oracle, and against the same rows run alone (T < 4096:
+    # standalone LayerNorms).
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg2"], num_hidden_layers=2), seed=26)
+    cfg = synth.flat_cfg(rl, enc)
+    D, F = cfg["hidden_size"], cfg["intermediate_size"]
+    rng = np.random.default_rng(27)
+    u = rng.standard_normal(F).astype(np.float32)
+    if offset == "row":
+        v = np.full(D, 20.0, np.float32)
+    else:
+        v = np.repeat(np.array([25.0, -20.0, 5.0], np.float32), D // 3)
+    for i in range(cfg["num_hidden_layers"]):
+        k = f"encoder.layers.{i}.mlp.Wo.weight"
+        w[k] = synth.bf16_round(w[k] + np.outer(v, u).astype(np.float32) / np.sqrt(F))
+    ids, mask, lens = synth.make_batch(12, 480, 380, 480, cfg["vocab_size"], seed=28)
+    assert int(lens.sum()) >= 4096
+    m = sj.Model(w, cfg, precision=BF16)
+    h = m.encode(ids, mask)
+    om = orc.model(w, cfg)
+    for b in (int(np.argmin(lens)), int(np.argmax(lens))):
+        n = int(lens[b])
+        ref = om.encode(ids[b:b + 1, :n], mask[b:b + 1, :n])[0]
+        err = float(np.abs(h[b, :n] - ref).max())
+        alone = m.encode(ids[b:b + 1, :n], mask[b:b + 1, :n])[0]
+        aerr = float(np.abs(alone - ref).max())
+        print(f"{offset} offsets: row {b} n={n} batch max|d|={err:.3g}, alone max|d|={aerr:.3g}", flush=True)
+        assert err <= TOL[BF16] and aerr <= TOL[BF16]
+    m.close()
+
+
 def test_more_than_256_sequences(orc):
     # More than 256 sequences: the sequence table, with the query-block prefix
     # that the attention work list is cut from, is filled on the host instead
