@@ -37,7 +37,9 @@ forward replayed as a captured hipGraph).  Also reported:
                    also the decision step over 8 typed questions per sequence
                    (256 rows, forward_shared, host arrays in and out).
 --legs selects the legs (default all: cfg3,b1,cfg4,cfg5,cpu); a run without
-cfg3 prints the other legs with a null value (profiling runs only).
+cfg3 prints the other legs with a null value (profiling runs only).  The
+extra leg `blas` (never by default) times config 3's four projection shapes
+as plain GEMMs with torch.matmul (hipBLASLt) beside sjh_gemm.
 """
 from __future__ import annotations
 
@@ -60,6 +62,7 @@ GEMM_NAMES = ("gemm_qkv_rope", "gemm_wo_resid", "gemm_wi_geglu", "gemm_wo2_resid
 
 PEAK_HBM_GBS = 8000.0
 LEGS = ("cfg3", "b1", "cfg4", "cfg5", "cpu")
+EXTRA_LEGS = ("blas",)  # run only when named
 
 # rocprofv3 --pmc summary of config 3 (FETCH_SIZE and WRITE_SIZE passes, each
 # scaled by the same counter on a plain copy of known size): lines
@@ -342,6 +345,51 @@ def b1_legs(sj, torch, w, cfg, stream):
              "graph_replays": gs["replays"], "p50_vs_fixed_shape": round(vp50 / p50, 4)})
 
 
+def blas_leg(sj, torch, T, D, F, stream, iters=50):
+    """The four projection products of config 3 (M = the batch's T valid
+    tokens) as plain bf16 GEMMs, out = A . W^T with no epilogue: torch.matmul
+    (hipBLASLt) beside this library's sjh_gemm on the same operands, each the
+    mean of `iters` launches between a hipEvent pair on the current stream.
+    A reference point for the GEMM kernels, not part of `value`."""
+    import ctypes as C
+
+    shapes = {"qkv": (3 * D, D), "wo": (D, D), "wi": (2 * F, D), "wo2": (D, F)}
+    g = torch.Generator(device="cuda").manual_seed(5)
+    out = {}
+    for name, (N, K) in shapes.items():
+        A = (torch.randn((T, K), device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+        W = (torch.randn((N, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        Cb = torch.empty((T, N), dtype=torch.bfloat16, device="cuda")
+        Cs = torch.empty_like(Cb)
+
+        def ours():
+            sj.check(sj.lib().sjh_gemm(C.c_void_p(A.data_ptr()), C.c_void_p(W.data_ptr()), None,
+                                       C.c_void_p(Cs.data_ptr()), T, N, K, 0, sj.SJH_BF16,
+                                       C.c_void_p(stream)))
+
+        def blas():
+            torch.matmul(A, W.t(), out=Cb)
+
+        res = {}
+        for label, fn in (("hipblaslt", blas), ("sjh", ours)):
+            for _ in range(5):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(iters):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / iters
+            tf = 2.0 * T * N * K / (us * 1e-6) / 1e12
+            res[label] = {"us": round(us, 2), "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+        res["max_abs_diff"] = float((Cb.float() - Cs.float()).abs().max())
+        out[name] = {"M": T, "N": N, "K": K, **res}
+        del A, W, Cb, Cs
+    return out
+
+
 def copy_probe(mib):
     """Plain device-to-device copy of a known size (torch's copy kernel): the
     calibration run for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -375,7 +423,7 @@ def main():
               "sequence with no exchange, but no multi-GPU path is built.", file=sys.stderr)
         sys.exit(2)
     legs = set(x.strip() for x in args.legs.split(",") if x.strip())
-    bad = legs - set(LEGS)
+    bad = legs - set(LEGS) - set(EXTRA_LEGS)
     if bad:
         ap.error(f"unknown legs {sorted(bad)}")
     for flag, leg in ((args.no_cpu, "cpu"), (args.no_latency, "b1"), (args.no_cfg4, "cfg4"),
@@ -440,6 +488,8 @@ def main():
                                   "per-row fp8 e4m3 projection weights (bf16 activations), batch "
                                   "32 x seq 1024, lengths U[256,1024] seed 1", "cfg5",
                                   sj.SJH_PREC_FP8W, 32, 1024, 256, 1024, 5, stream, questions=8)
+    if "blas" in legs:
+        extra["blas_cfg3_shapes"] = blas_leg(sj, torch, T, D, F, stream)
     cpu = cpu_baseline(w, rl, enc, ids, mask, lens, NL) if "cpu" in legs else None
     out = {
         "metric": METRIC, "value": round(value, 1) if value else None, "unit": "tokens/s",
