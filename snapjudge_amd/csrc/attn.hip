@@ -224,18 +224,27 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     constexpr int MASK = decltype(mask_tag)::value;
     constexpr bool NOMAX = decltype(nomax_tag)::value;
     static_assert(PRE || !NOMAX, "the offset-free pass needs log2-domain logits");
-    // S^T[key][query] for keys kt + [0, 32) and kt + [32, 64)
     f32x16_t s[2];
+    // S^T[key][query] for keys kt + [0, 32) and kt + [32, 64): every K
+    // fragment of the tile is read first, then the two accumulators' MFMAs
+    // go in turn (reading each fragment just before its MFMA left a wait on
+    // the LDS between MFMAs; the V^T fragments stay where they are used:
+    // holding them from here needs more registers than three workgroups per
+    // CU leave)
+    bf16x8_t kf[2][4];
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) kf[jb][st] = *reinterpret_cast<const bf16x8_t*>(sb + jb * 4096 + koff[st]);
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[jb][e] = 0.f;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(sb + jb * 4096 + koff[st]);
-        s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[jb], 0, 0, 0);
-      }
-    }
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[jb][st], qf[st], s[jb], 0, 0, 0);
     static_assert(!(NOMAX && MASK == 1), "the offset-free pass takes the last tile unmasked");
     if constexpr (MASK != 0) {
       // key of element (jb, e) is kt + 4*hb + 32*jb + 8*(e/4) + e%4
