@@ -16,6 +16,10 @@ namespace sjh {
 namespace {
 
 constexpr int kLnWaves = 4;        // rows per workgroup
+#ifndef SJH_LN_PARTS_WAVES
+#define SJH_LN_PARTS_WAVES 1
+#endif
+constexpr int kLnPartsWaves = SJH_LN_PARTS_WAVES;  // rows per workgroup of the split-K sums
 constexpr int kLnMaxPerLane = 64;  // D <= 4096 (64 lanes x 64 values)
 
 // LayerNorm as src/tensor.cpp:54-79: mean and population variance
@@ -166,11 +170,11 @@ __device__ __forceinline__ void wave_sum2(double& a, double& b) {
 // src/tensor.cpp:63-71 (mean and population variance in double, inverse std
 // rounded to float), gathered in one pass as the moments of x - x0 (x0 =
 // the row's first value, which keeps E[d^2] - E[d]^2 well conditioned).
-template <int NV, bool FULL, typename InT, typename ResT, typename OutT>
-__global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
+template <int NV, bool FULL, typename InT, typename ResT, typename OutT, int WPB>
+__global__ __launch_bounds__(64 * WPB) void ln_vec_kernel(LnArgs a) {
   const int lane = threadIdx.x & 63;
   // The row is uniform over the wave: scalar row addresses and gather index.
-  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * kLnWaves + (threadIdx.x >> 6));
+  const int r = __builtin_amdgcn_readfirstlane(blockIdx.x * WPB + (threadIdx.x >> 6));
   if (r >= (a.M_dev ? *a.M_dev : a.M)) return;
   const int D = a.D, nch = D >> 2;
   const int64_t src_row = a.ids ? static_cast<int64_t>(a.ids[r]) : static_cast<int64_t>(r);
@@ -321,14 +325,18 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_vec_kernel(LnArgs a) {
 
 template <int NV, typename InT, typename ResT>
 void ln_vec_dispatch_out(const LnArgs& a, hipStream_t st) {
-  dim3 grid((a.M + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
+  // Rows (waves) per workgroup.  The split-K partial sums run on short
+  // batches only (M <= 256): each row there streams its partial rows, so
+  // the rows are spread over kLnPartsWaves-wave workgroups.
+  constexpr int WPB = std::is_same<ResT, PartsRes>::value ? kLnPartsWaves : kLnWaves;
+  dim3 grid((a.M + WPB - 1) / WPB), block(64 * WPB);
   const bool full = a.D == 256 * NV;
   if (a.y_dtype == DT_BF16)
-    full ? ln_vec_kernel<NV, true, InT, ResT, bf16_t><<<grid, block, 0, st>>>(a)
-         : ln_vec_kernel<NV, false, InT, ResT, bf16_t><<<grid, block, 0, st>>>(a);
+    full ? ln_vec_kernel<NV, true, InT, ResT, bf16_t, WPB><<<grid, block, 0, st>>>(a)
+         : ln_vec_kernel<NV, false, InT, ResT, bf16_t, WPB><<<grid, block, 0, st>>>(a);
   else
-    full ? ln_vec_kernel<NV, true, InT, ResT, float><<<grid, block, 0, st>>>(a)
-         : ln_vec_kernel<NV, false, InT, ResT, float><<<grid, block, 0, st>>>(a);
+    full ? ln_vec_kernel<NV, true, InT, ResT, float, WPB><<<grid, block, 0, st>>>(a)
+         : ln_vec_kernel<NV, false, InT, ResT, float, WPB><<<grid, block, 0, st>>>(a);
 }
 
 template <typename InT, typename ResT>
