@@ -89,12 +89,46 @@ __device__ __forceinline__ void load_lds16_buf(__amdgpu_buffer_rsrc_t r, uint32_
                                            static_cast<int>(voff), static_cast<int>(soff), 0, 0);
 }
 
-// Transposed 8-byte LDS read (ds_read_b64_tr_b16).  Within each 16-lane
-// group, if lane q + 4k addresses element (r0 + k, c0 + 4q) of a row-major
-// tile, lane i of the group receives elements (r0 + k, c0 + i), k = 0..3.
-__device__ __forceinline__ s16x4_t lds_read_tr(const char* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4_t*)(p));
+// Transposed 8-byte LDS read (ds_read_b64_tr_b16) at LDS byte address
+// addr + OFF.  Within each 16-lane group, if lane q + 4k addresses element
+// (r0 + k, c0 + 4q) of a row-major tile, lane i of the group receives
+// elements (r0 + k, c0 + i), k = 0..3.
+//
+// Inline asm rather than the builtin: before the builtin's read the compiler
+// waits for every direct-to-LDS load in flight (vmcnt(0)), which would hold
+// each tile's P.V phase until the next tile's K/V loads (into the other ring
+// slot) have landed.  The asm is invisible to the compiler's wait insertion,
+// so its results are claimed with lgkm_claim before their first use.
+template <int OFF>
+__device__ __forceinline__ s16x4_t lds_read_tr(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  s16x4_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return r;
+}
+// Waits until at most N LDS operations of this wave are outstanding, tied to
+// the four registers it makes valid (the compiler cannot move their uses
+// above it).  LDS operations complete in issue order, so N = the number of
+// LDS reads issued after the four means those four have returned; LDS
+// operations the compiler issues in between only make the wait longer.
+template <int N>
+__device__ __forceinline__ void lgkm_claim(s16x4_t& a, s16x4_t& b, s16x4_t& c, s16x4_t& d) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt immediate");
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
+}
+// f(integral_constant<int, I>) for I = B .. E - 1 in turn: loop indices that
+// the asm operands above need as compile-time constants.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+// LDS byte address of a pointer into the workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
 }
 
 // Register budget for three workgroups per CU (168 VGPRs, 3 waves per SIMD):
@@ -201,9 +235,10 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
   // keys 4 * (g / 2) + [0, 4) of an 8-key half step.  The swizzle key of a
   // row, a function of (row >> 1) & 7, does not see the 32-row block jb or
   // the 16-row step u, so those enter as constants (folded into the LDS
-  // instructions' offset fields): koff[st] + 4096 jb, voff[db][hl] + 4096 jb
-  // + 2048 u.
-  int koff[4], voff[2][2];
+  // instructions' offset fields): koff[st] + 4096 jb; the V reads take the
+  // LDS address vaddr[db][hl] (stage 0) plus slot * kStage + 4096 jb + 2048 u.
+  int koff[4];
+  uint32_t vaddr[2][2];
   {
     const int tq = lane & 3, tk = (lane >> 2) & 3, tg = lane >> 4;
     const int tdim = 16 * (tg & 1) + 4 * tq;
@@ -213,16 +248,21 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int hl = 0; hl < 2; ++hl) voff[db][hl] = kKey * 128 + kv_off(8 * hl + tkey, db * 32 + tdim);
+      for (int hl = 0; hl < 2; ++hl)
+        vaddr[db][hl] = lds_addr(smem) + kKey * 128 + kv_off(8 * hl + tkey, db * 32 + tdim);
   }
 
   // One 64-key tile at key offset kt from the stage at sb.  MASK 0: interior
   // tile of full attention; 1: its last tile (keys >= qhi masked); 2: a
   // sliding window (keys outside [qlo, qhi) masked).  NOMAX (PRE only): the
   // exp2 offset stays 0 and no tile max is taken (see the pass check below).
-  auto tile = [&](auto mask_tag, auto nomax_tag, const char* sb, int kt) {
+  // ST >= 0: the tile's ring slot, known to the caller (folded into the LDS
+  // offsets); ST < 0: slot `slot`.
+  auto tile = [&](auto mask_tag, auto nomax_tag, auto slot_tag, int slot, int kt) {
     constexpr int MASK = decltype(mask_tag)::value;
     constexpr bool NOMAX = decltype(nomax_tag)::value;
+    constexpr int ST = decltype(slot_tag)::value;
+    const char* sb = smem + (ST >= 0 ? ST : slot) * kStage;
     static_assert(PRE || !NOMAX, "the offset-free pass needs log2-domain logits");
     f32x16_t s[2];
     // S^T[key][query] for keys kt + [0, 32) and kt + [32, 64): every K
@@ -311,28 +351,49 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     // O^T[dim][query] += V^T[dim][key] . P^T[key][query].  The MFMA's k index
     // 8 * hb + t of a 16-key step u stands for key 16u + 4hb + t (t < 4) or
     // 16u + 8 + 4hb + (t - 4): the order in which the S^T accumulator holds
-    // them, so P^T needs no data movement and V^T is read to match.
+    // them, so P^T needs no data movement and V^T is read to match.  The
+    // V^T reads go in groups g = 2 jb + u of four, two groups ahead of the
+    // MFMAs: group g + 2 is issued after group g's MFMAs, so exactly one
+    // group (four reads) is issued after each group but the last when its
+    // MFMAs wait for it.
+    uint32_t vb[2][2];
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        bf16x8_t pf;
+      for (int hl = 0; hl < 2; ++hl) vb[db][hl] = ST >= 0 ? vaddr[db][hl] : vaddr[db][hl] + slot * kStage;
+    constexpr int SOFF = ST >= 0 ? ST * kStage : 0;
+    s16x4_t vr[4][2][2];
+    auto vread = [&](auto g_tag) {
+      constexpr int g = decltype(g_tag)::value;
+      constexpr int off = SOFF + (g >> 1) * 4096 + (g & 1) * 2048;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pf[e] = static_cast<__bf16>(s[jb][8 * u + e]);
-        const bf16x2_t ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
-        l_i = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[0], pf[1]}, ones, l_i, false);
-        l_j = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[2], pf[3]}, ones, l_j, false);
-        l_i = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[4], pf[5]}, ones, l_i, false);
-        l_j = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[6], pf[7]}, ones, l_j, false);
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const s16x4_t lo = lds_read_tr(sb + jb * 4096 + u * 2048 + voff[db][0]);
-          const s16x4_t hi = lds_read_tr(sb + jb * 4096 + u * 2048 + voff[db][1]);
-          const bf16x8_t vf = __builtin_bit_cast(
-              bf16x8_t, (s16x8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
-        }
+      for (int db = 0; db < 2; ++db) {
+        vr[g][db][0] = lds_read_tr<off>(vb[db][0]);
+        vr[g][db][1] = lds_read_tr<off>(vb[db][1]);
       }
+    };
+    vread(std::integral_constant<int, 0>{});
+    vread(std::integral_constant<int, 1>{});
+    static_for<0, 4>([&](auto g_tag) {
+      constexpr int g = decltype(g_tag)::value, jb = g >> 1, u = g & 1;
+      bf16x8_t pf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf[e] = static_cast<__bf16>(s[jb][8 * u + e]);
+      const bf16x2_t ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+      l_i = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[0], pf[1]}, ones, l_i, false);
+      l_j = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[2], pf[3]}, ones, l_j, false);
+      l_i = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[4], pf[5]}, ones, l_i, false);
+      l_j = __builtin_amdgcn_fdot2_f32_bf16((bf16x2_t){pf[6], pf[7]}, ones, l_j, false);
+      lgkm_claim<g < 3 ? 4 : 0>(vr[g][0][0], vr[g][0][1], vr[g][1][0], vr[g][1][1]);
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const s16x4_t lo = vr[g][db][0], hi = vr[g][db][1];
+        const bf16x8_t vf = __builtin_bit_cast(
+            bf16x8_t, (s16x8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
+      }
+      if constexpr (g + 2 < 4) vread(std::integral_constant<int, g + 2>{});
+    });
   };
 
   // ST: the ring slot of tile t when the caller knows it (t % kNS), so the
@@ -347,7 +408,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
       wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
     if (t + kNS - 1 < ntiles) issue(t + kNS - 1, ST >= 0 ? (ST + kNS - 1) % kNS : (t + kNS - 1) % kNS);
-    if (wave_active) tile(mask_tag, nomax_tag, smem + slot * kStage, klo + t * kKey);
+    if (wave_active) tile(mask_tag, nomax_tag, slot_tag, slot, klo + t * kKey);
   };
   // One pass over the item's key tiles.  The interior tiles of full attention
   // run in a loop of their own, then the masked ones: no branch between the
