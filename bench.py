@@ -57,7 +57,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "encoder tokens/sec at B64×S512 bf16 (1 GPU); attention MFMA % peak; p50 latency at B1"
 PEAK_BF16_TFLOPS = 2500.0
-GEMM_NAMES = ("gemm_qkv_rope", "gemm_wo_resid", "gemm_wi_geglu", "gemm_wo2_resid")
+GEMM_NAMES = ("gemm_qkv_rope", "gemm_wo_resid", "gemm_wi_geglu", "gemm_wo2_resid", "gemm_wo_resid_ln",
+              "gemm_wo2_resid_ln")
 
 
 PEAK_HBM_GBS = 8000.0
@@ -86,11 +87,14 @@ def measured_traffic(path, group):
 # launch one kernel instantiation (rocprofv3 reports them as one kernel).
 KERNEL_GROUPS = {
     "gemm_qkv_rope": (("gemm_qkv_rope",), "gemm_bf16_pers_kernel<256, 256, 4, 4, 2, 64, false, 2, "
-                      "unsigned short> (QKV projection + RoPE epilogue)", "mfma"),
+                      "unsigned short, 0> (QKV projection + RoPE epilogue)", "mfma"),
     "gemm_wi_geglu": (("gemm_wi_geglu",), "gemm_bf16_pers_kernel<256, 256, 4, 4, 2, 64, false, 3, "
-                      "unsigned short> (Wi projection + GEGLU epilogue)", "mfma"),
+                      "unsigned short, 0> (Wi projection + GEGLU epilogue)", "mfma"),
+    "gemm_resid_ln": (("gemm_wo_resid_ln", "gemm_wo2_resid_ln"), "gemm_bf16_pers_kernel<256, 256, 4, 4, "
+                      "2, 64, false, 1, float, 3> (Wo and Wo2 projections + residual + LayerNorm epilogue)",
+                      "mfma"),
     "gemm_resid": (("gemm_wo_resid", "gemm_wo2_resid"), "gemm_bf16_pers_kernel<256, 256, 4, 4, 2, "
-                   "64, false, 1, float> (Wo and Wo2 projections + residual epilogue)", "mfma"),
+                   "64, false, 1, float, 0> (Wo and Wo2 projections + residual epilogue)", "mfma"),
     "attention": (("attention",), "attn_bf16_mfma_kernel (varlen flash attention)", "mfma"),
     "layer_norm": (("attn_norm", "mlp_norm", "final_norm"), "ln_vec_kernel<3, true, float, NoRes, "
                    "unsigned short> (fp32 rows -> bf16 LayerNorm)", "hbm"),
@@ -105,6 +109,8 @@ def role_work(role, T, D, F, sum_n2):
         "gemm_wi_geglu": (2.0 * T * D * 2 * F, 2.0 * (T * D + 2 * F * D + T * F)),
         "gemm_wo_resid": (2.0 * T * D * D, 2.0 * (T * D + D * D) + 8.0 * T * D),
         "gemm_wo2_resid": (2.0 * T * F * D, 2.0 * (T * F + D * F) + 8.0 * T * D),
+        "gemm_wo_resid_ln": (2.0 * T * D * D, 2.0 * (T * D + D * D) + 10.0 * T * D),
+        "gemm_wo2_resid_ln": (2.0 * T * F * D, 2.0 * (T * F + D * F) + 10.0 * T * D),
         "attention": (4.0 * D * sum_n2, 8.0 * T * D),
         "attn_norm": (0.0, 6.0 * T * D),
         "mlp_norm": (0.0, 6.0 * T * D),

@@ -106,6 +106,13 @@ typedef struct sjh_options {
                          encode() returns its values at padded positions too; 0: work
                          only on valid tokens (padded positions of encode() are 0) */
   int32_t device;     /* HIP device ordinal */
+  int32_t fuse_ln;    /* 1 (default): where a residual GEMM's tiles all run at once (bf16,
+                         hidden size a multiple of 256 up to 1024, one round of tiles), its
+                         epilogue also writes the LayerNorm that reads the residual stream
+                         next; 0: that LayerNorm runs as a launch of its own; 2: as 1, but a
+                         tile waits for its panel's other tiles for one poll only, so that
+                         most tiles take the path of a tile that gave up waiting (the
+                         results are the same bits as with 1; for tests) */
 } sjh_options;
 
 typedef struct sjh_model sjh_model;

@@ -232,6 +232,8 @@ Engine::Engine(const ModelSource& src, const sjh_options& o) {
   w8_ = prec_ == SJH_PREC_FP8W;
   use_graphs_ = o.use_graphs != 0;
   pad_rows_ = o.pad_rows != 0;
+  rln_ = o.fuse_ln != 0;
+  rln_spin_ = o.fuse_ln == 2 ? 1 : kRlnSpin;
 
   arch_ = src.arch;
   act_head_ = src.act_head;
@@ -472,6 +474,9 @@ void Engine::stage_weights(const ModelSource& s) {
   // on the CPU).  The standalone LayerNorms run instead.
   ln_fold_ = kLnFoldEnabled && act_dt_ == DT_BF16 && !bert && D % kLnBlock == 0 &&
              D / kLnBlock <= kLnMaxBlocks && Dh_ == 64 && F % 128 == 0;
+  // The residual GEMMs' epilogues finish the next LayerNorm (GemmArgs::rln_y)
+  // on the bf16-weight persistent path, for D a multiple of 256 up to 1024.
+  rln_ = rln_ && act_dt_ == DT_BF16 && !w8_ && !bert && D % kLnBlock == 0 && D / kLnBlock <= kLnMaxBlocks;
   if (ln_fold_) {
     for (auto& L : layers_) {
       const int wdt = w8_ ? DT_FP8 : DT_BF16;
@@ -674,6 +679,14 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   if (n_pairs > 0) attn_part_.ensure(static_cast<size_t>(n_pairs) * 2 * kAttnPartFloats * 4);
   // moments of every 256-row tile the persistent kernel reads, one tile past the last
   if (ln_fold_) ln_stats_.ensure(((t + 255) / 256 * 256 + 256) * static_cast<size_t>(D / kLnBlock) * 8);
+  if (rln_) {
+    // the sync ints start at zero and every launch leaves them at zero
+    rln_mom_.ensure(t * static_cast<size_t>(D / kLnBlock) * 16);
+    const size_t sync_bytes = (t + 255) / 256 * kRlnSyncInts * 4;
+    rln_sync_.ensure(sync_bytes);
+    hip_check(hipMemsetAsync(rln_sync_.get(), 0, rln_sync_.bytes(), stream_), "clear LayerNorm sync ints");
+    hip_check(hipStreamSynchronize(stream_), "clear LayerNorm sync ints");
+  }
   X_.ensure(t * D * 4);
   Y_.ensure(t * D * as);
   QKV_.ensure(t * 3 * D * as);
@@ -702,6 +715,8 @@ void Engine::ensure_workspace(int Tb, int Bb) {
   ws_.attn_part = n_pairs > 0 ? attn_part_.as<float>() : nullptr;
   ws_.attn_pairs_cap = n_pairs;
   ws_.ln_stats = ln_fold_ ? ln_stats_.as<float>() : nullptr;
+  ws_.rln_mom = rln_ ? rln_mom_.as<float>() : nullptr;
+  ws_.rln_sync = rln_ ? rln_sync_.as<int>() : nullptr;
   ++ws_gen_;
   for (auto& kv : graphs_) drop_graph(kv.second);  // every launch ended (above)
   graphs_.clear();
@@ -844,6 +859,25 @@ void Engine::resid_gemm_ln(const char* gname, const GemmArgs& g0, const char* ln
     a = folded;
   }
   ln(lname, a, st);
+}
+
+bool Engine::rln_resid(GemmArgs& g, const LnArgs& a, const Ws& w) const {
+  // a plain LayerNorm of X's rows into bf16 Y (the attn_norm and mlp_norm
+  // steps), on a launch whose tiles all run at once
+  if (!rln_ || !w.rln_mom || !w.rln_sync || !a.normalize || !a.w || a.in != g.X || a.ld_in != g.ldx ||
+      a.in_dtype != DT_F32 || a.y_dtype != DT_BF16 || !a.y_out || a.x_out || a.xio || a.resid || a.ids ||
+      a.add || a.M != g.M || a.D != g.N)
+    return false;
+  if (!gemm_takes_rln(g)) return false;
+  g.rln_y = a.y_out;
+  g.rln_ldy = a.ld_y;
+  g.rln_w = a.w;
+  g.rln_b = a.b;
+  g.rln_eps = a.eps;
+  g.rln_mom = w.rln_mom;
+  g.rln_sync = w.rln_sync;
+  g.rln_spin = rln_spin_;
+  return true;
 }
 
 void Engine::ln(const char* name, const LnArgs& a, hipStream_t st) {
@@ -1094,6 +1128,8 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
         g.ln_w = ly.mlp_norm.as<float>();
         g.ln_stats_out = w.ln_stats;
         gemm("gemm_wo_resid", g, w, st);
+      } else if (rln_resid(g, a, w)) {
+        gemm("gemm_wo_resid_ln", g, w, st);
       } else {
         resid_gemm_ln("gemm_wo_resid", g, "mlp_norm", a, w, st);
       }
@@ -1154,7 +1190,11 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
         g.ln_stats_out = w.ln_stats;
         gemm("gemm_wo2_resid", g, w, st);
       } else if (li + 1 < nlayers_) {
-        resid_gemm_ln("gemm_wo2_resid", g, "attn_norm", attn_norm_args(li + 1), w, st);
+        const LnArgs a = attn_norm_args(li + 1);
+        if (rln_resid(g, a, w))
+          gemm("gemm_wo2_resid_ln", g, w, st);
+        else
+          resid_gemm_ln("gemm_wo2_resid", g, "attn_norm", a, w, st);
       } else {
         resid_gemm_ln("gemm_wo2_resid", g, "final_norm", final_args, w, st);
       }

@@ -102,6 +102,11 @@ struct Ws {
   float* attn_part = nullptr;     // partials of key-split items (AttnArgs::part), or none
   int attn_pairs_cap = 0;         // split items they hold
   float* ln_stats = nullptr;      // row moments of a folded LayerNorm (GemmArgs::ln_stats_out), or none
+  // the LayerNorm finished by the residual epilogue (GemmArgs::rln_y): row
+  // moments [Tb][D / 256][4] and kRlnSyncInts zeroed ints per 256-row panel,
+  // or none
+  float* rln_mom = nullptr;
+  int* rln_sync = nullptr;
 };
 
 class Engine {
@@ -205,6 +210,12 @@ class Engine {
   // batches the split-K residual epilogue is folded into that layer norm.
   void resid_gemm_ln(const char* gname, const GemmArgs& g, const char* lname, LnArgs a,
                      const Ws& w, hipStream_t st);
+  // Sets g up to finish the LayerNorm a (of X's rows into bf16 Y) in its
+  // residual epilogue (GemmArgs::rln_y) and returns true where that applies;
+  // false leaves g as it was.
+  bool rln_resid(GemmArgs& g, const LnArgs& a, const Ws& w) const;
+  // polls of a panel's arrival count before a tile gives up waiting
+  static constexpr int kRlnSpin = 20000;
   void attn(const char* name, const AttnArgs& a, hipStream_t st);
   void prof_begin(hipStream_t st);
   void prof_end(const char* name, hipStream_t st);
@@ -227,6 +238,10 @@ class Engine {
   // the encoder's LayerNorms after its residual GEMMs can fold into them and
   // the next GEMMs (GemmArgs::ln_y) on the persistent kernel's batches
   bool ln_fold_ = false;
+  // the residual GEMMs' epilogues finish the LayerNorm that reads X next
+  // where their tiles all run at once (sjh_options::fuse_ln)
+  bool rln_ = false;
+  int rln_spin_ = 0;  // GemmArgs::rln_spin
   int arch_ = ARCH_MODERNBERT;  // ModernBERT (DecisionModel) or BERT (SjModel)
   int act_head_ = ACT_MLP;
   int head_ff_ = 0, head_act_ = 2;
@@ -252,6 +267,7 @@ class Engine {
   DevBuf attn_items_;  // attention work list (AttnArgs::items)
   DevBuf attn_part_;   // partials of key-split attention items (AttnArgs::part)
   DevBuf ln_stats_;    // folded LayerNorm row moments (Ws::ln_stats)
+  DevBuf rln_mom_, rln_sync_;  // Ws::rln_mom, Ws::rln_sync
   Ws ws_;          // views of the buffers above
   DevBuf tail_idx_, tail_rows_, tail_s0_, tail_s1_, tail_s2_, tail_lg_, tail_ain_, tail_ah_,
       tail_ao_, tail_act_;

@@ -645,6 +645,239 @@ __device__ __forceinline__ void ln_fold_acc(const GemmArgs& g, f32x16_t (&acc)[T
   }
 }
 
+// ---- the next LayerNorm finished in the residual epilogue ------------------
+// (GemmArgs::rln_y).  With every tile of the launch in a workgroup of its own
+// and all of them resident, the N / 256 tiles of a 256-row panel hold whole
+// rows of the updated residual stream x between them.  Each tile publishes
+// its rows' moments over its 256 columns (mean and sum of squared
+// deviations from it, fp32), counts itself into the panel's arrival counter
+// and waits until every tile of the panel has arrived; it then combines the
+// panel's moments per row in double (src/tensor.cpp:63-71: mean and
+// population variance, the inverse std rounded to float) and writes LN(x) of
+// its own block from the registers, with launch_ln's arithmetic.  The wait is
+// bounded (rln_spin polls): a tile that gives up marks its block, and the
+// panel's last tile to finish normalises the marked blocks from X in memory
+// with the same published moments, so the result does not depend on which
+// way it went.  Sync ints of panel p (kRlnSyncInts from 8p): [0] arrivals,
+// [1] finishes, [2 + b] block b given up; the last tile to finish clears
+// them for the next launch.
+//
+// Memory ordering: the moments and the sync ints are agent-scope atomics
+// (written through to, and read from, the level every XCD sees).  A tile's
+// moment stores have completed (vmcnt) before its arrival is counted, and
+// the moment loads are issued only after the count was seen complete.  Only
+// the give-up path needs X itself seen by another workgroup: a release fence
+// before the mark, an acquire fence before the last tile reads X.
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Row statistics (float mean, inverse std) of row m from the nb blocks'
+// published (x0, s, q) (ln_block_combine's arithmetic).
+__device__ __forceinline__ void rln_row_stats(const GemmArgs& g, int m, int nb, float& fmean, float& finv) {
+  const float* p = g.rln_mom + static_cast<int64_t>(m) * nb * 4;
+  float x0[kLnStatMaxBlocks] = {}, sb[kLnStatMaxBlocks] = {}, qb[kLnStatMaxBlocks] = {};
+#pragma unroll
+  for (int b = 0; b < kLnStatMaxBlocks; ++b)
+    if (b < nb) {
+      x0[b] = __hip_atomic_load(p + 4 * b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sb[b] = __hip_atomic_load(p + 4 * b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      qb[b] = __hip_atomic_load(p + 4 * b + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  ln_block_combine(x0, sb, qb, nb, g.rln_eps, fmean, finv);
+}
+
+// Every wave of the workgroup calls it (it holds barriers).  lds: (WGN + 3)
+// * BM floats and 4 ints past the ring.
+template <int BM, int BN, int WM, int WN, int TI, int TJ, int WGN>
+__device__ __forceinline__ void resid_rln_epilogue(const GemmArgs& g, f32x16_t (&acc)[TI][TJ], int m0, int tile_m,
+                                                   int tile_n, int wm, int wn, int l32, int hb, int tid, char* lds) {
+  static_assert(BM == 256 && BN == kLnBlock && TJ == 2 && WN == 64 && WM == 32 * TI,
+                "the 16-wave 256 x 256 tile of 64 x 64 waves");
+  float* red = reinterpret_cast<float*>(lds);  // [WGN][BM] partial sums
+  float* mu = red + WGN * BM;                  // [BM] the block's shifted means s, then the rows' means
+  float* rinv = mu + BM;                       // [BM] the rows' inverse std
+  float* x0s = rinv + BM;                      // [BM] the block's first value of each row
+  int* flag = reinterpret_cast<int*>(x0s + BM);  // [0] panel complete, [1] last to finish, [2] blocks given up
+  const int nb = g.N / BN;
+  const int c0 = tile_n * BN + wn * WN;
+  const int rw = m0 + wm * WM;             // the wave's first row
+  const int rows_in = min(g.M - rw, WM);   // its rows below M (may be <= 0)
+  const uint32_t ld4 = static_cast<uint32_t>(g.ldx) * 4u;
+  const uint32_t lo4 = 4 * hb * ld4 + l32 * 4;
+  char* xw = reinterpret_cast<char*>(g.X + static_cast<int64_t>(rw) * g.ldx + c0);
+  int* sync = g.rln_sync + kRlnSyncInts * tile_m;
+  // lane (l32, hb) holds rows i * 32 + 8 (e / 4) + 4 hb + e % 4 of the wave,
+  // columns j * 32 + l32
+  auto rowof = [&](int i, int e) { return i * 32 + 8 * (e >> 2) + (e & 3) + 4 * hb; };
+
+  // 1) X += acc + bias, the sum x kept in acc; the X reads of a group of 8
+  //    rows go out before the first add (as in the plain residual epilogue)
+  float bv[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) bv[j] = g.bias ? g.bias[c0 + j * 32 + l32] : 0.f;
+  constexpr int RG = 8;
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int e0 = 0; e0 < 16; e0 += RG) {
+      float xv[RG][TJ];
+#pragma unroll
+      for (int e = 0; e < RG; ++e) {
+        const int r = rowof(i, e0 + e);
+        const char* xr = xw + static_cast<uint32_t>((r - 4 * hb) * ld4 + lo4);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) xv[e][j] = r < rows_in ? *reinterpret_cast<const float*>(xr + j * 128) : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < RG; ++e) {
+        const int r = rowof(i, e0 + e);
+        char* xr = xw + static_cast<uint32_t>((r - 4 * hb) * ld4 + lo4);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          acc[i][j][e0 + e] = xv[e][j] + (acc[i][j][e0 + e] + bv[j]);
+          if (r < rows_in) *reinterpret_cast<float*>(xr + j * 128) = acc[i][j][e0 + e];
+        }
+      }
+    }
+
+  // 2) the rows' block moments (ln_block_combine's inputs): the shift x0 is
+  //    the block's first column (wave wn = 0, lane column 0); the pairwise
+  //    tree is the wave's two column blocks (columns k, k + 32), rows16_sum
+  //    over its 32 lane columns (distances 16 .. 1), then the four column
+  //    waves as (g0 + g1) + (g2 + g3)
+  if (wn == 0 && l32 == 0) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x0s[wm * WM + rowof(i, e)] = acc[i][0][e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4_t x4 = *reinterpret_cast<const f32x4_t*>(x0s + wm * WM + i * 32 + 8 * q + 4 * hb);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[4 * q + t] = (acc[i][0][4 * q + t] - x4[t]) + (acc[i][1][4 * q + t] - x4[t]);
+    }
+    const float sum = rows16_sum(v, l32);
+    if ((l32 & 1) == 0) red[wn * BM + wm * WM + i * 32 + rows16_row(l32, hb)] = sum;
+  }
+  __syncthreads();
+  static_assert(WGN == 4, "the four 64-column groups combine as (g0 + g1) + (g2 + g3)");
+  if (tid < BM) mu[tid] = ((red[tid] + red[BM + tid]) + (red[2 * BM + tid] + red[3 * BM + tid])) * (1.0f / BN);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4_t x4 = *reinterpret_cast<const f32x4_t*>(x0s + wm * WM + i * 32 + 8 * q + 4 * hb);
+      const f32x4_t s4 = *reinterpret_cast<const f32x4_t*>(mu + wm * WM + i * 32 + 8 * q + 4 * hb);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float e0 = (acc[i][0][4 * q + t] - x4[t]) - s4[t], e1 = (acc[i][1][4 * q + t] - x4[t]) - s4[t];
+        v[4 * q + t] = ln_pair_sq(e0, e1);
+      }
+    }
+    const float ss = rows16_sum(v, l32);
+    if ((l32 & 1) == 0) red[wn * BM + wm * WM + i * 32 + rows16_row(l32, hb)] = ss;
+  }
+  __syncthreads();
+  if (tid < BM && m0 + tid < g.M) {
+    const float q = (red[tid] + red[BM + tid]) + (red[2 * BM + tid] + red[3 * BM + tid]);
+    float* p = g.rln_mom + (static_cast<int64_t>(m0 + tid) * nb + tile_n) * 4;
+    __hip_atomic_store(p, x0s[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 1, mu[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 2, q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  wait_vm_all();  // this thread's X and moment stores have completed
+  __syncthreads();
+
+  // 3) count the tile in (its X stores and moment stores have completed)
+  if (tid == 0) __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    int n = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int it = 0; n < nb && it < g.rln_spin; ++it) {
+      __builtin_amdgcn_s_sleep(2);
+      n = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    flag[0] = n >= nb;
+  }
+  __syncthreads();
+
+  const bool has_b = g.rln_b != nullptr;
+  bf16_t* yw = static_cast<bf16_t*>(g.rln_y) + static_cast<int64_t>(rw) * g.rln_ldy + c0 + l32;
+  if (__builtin_amdgcn_readfirstlane(flag[0])) {  // uniform
+    // 4) every tile of the panel has published its moments
+    if (tid < BM && m0 + tid < g.M) rln_row_stats(g, m0 + tid, nb, mu[tid], rinv[tid]);
+    __syncthreads();
+    float lw[TJ], lb[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      lw[j] = g.rln_w[c0 + j * 32 + l32];
+      lb[j] = has_b ? g.rln_b[c0 + j * 32 + l32] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4_t fm = *reinterpret_cast<const f32x4_t*>(mu + wm * WM + i * 32 + 8 * q + 4 * hb);
+        const f32x4_t fi = *reinterpret_cast<const f32x4_t*>(rinv + wm * WM + i * 32 + 8 * q + 4 * hb);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int r = rowof(i, 4 * q + t);
+          if (r >= rows_in) continue;
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            yw[static_cast<int64_t>(r) * g.rln_ldy + j * 32] =
+                f32_to_bf16(ln_apply(acc[i][j][4 * q + t], fm[t], fi[t], lw[j], lb[j], has_b));
+        }
+      }
+  } else {
+    // 4') gave up waiting: X of this block to where the panel's last tile
+    //     reads it, then the block's mark
+    wait_vm_all();
+    __syncthreads();
+    if (tid == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __hip_atomic_store(sync + 2 + tile_n, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  wait_vm_all();
+  __syncthreads();
+
+  // 5) the panel's last tile to finish normalises the blocks given up, then
+  //    clears the panel's sync ints
+  if (tid == 0) {
+    const int old = __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flag[1] = old == nb - 1;
+    int given_up = 0;
+    if (old == nb - 1)
+      for (int b = 0; b < nb; ++b)
+        given_up |= __hip_atomic_load(sync + 2 + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) << b;
+    flag[2] = given_up;
+  }
+  __syncthreads();
+  const int last = __builtin_amdgcn_readfirstlane(flag[1]), given_up = __builtin_amdgcn_readfirstlane(flag[2]);
+  if (last && given_up) {  // uniform; rarely taken
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (tid < BM && m0 + tid < g.M) rln_row_stats(g, m0 + tid, nb, mu[tid], rinv[tid]);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+      if (!((given_up >> b) & 1)) continue;
+      for (int k = tid; k < BM * BN; k += 64 * WGN * (BM / WM)) {
+        const int r = k / BN, c = b * BN + k % BN;
+        if (m0 + r >= g.M) continue;
+        const float x = g.X[static_cast<int64_t>(m0 + r) * g.ldx + c];
+        static_cast<bf16_t*>(g.rln_y)[static_cast<int64_t>(m0 + r) * g.rln_ldy + c] =
+            f32_to_bf16(ln_apply(x, mu[r], rinv[r], g.rln_w[c], has_b ? g.rln_b[c] : 0.f, has_b));
+      }
+    }
+  }
+  if (last && tid < 2 + nb) __hip_atomic_store(sync + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---- direct-to-LDS variant -------------------------------------------------
 // Tiles move from HBM to LDS with global_load_lds_dwordx4 (no VGPR staging):
 // lane l of an instruction writes its 16 bytes at LDS address base + 16*l, so
@@ -1119,9 +1352,12 @@ void gemm_bf16_pers_kernel(GemmArgs g0) {
   const int lo = static_cast<int>(static_cast<int64_t>(tiles) * offx / nwg);
   const int hi = static_cast<int>(static_cast<int64_t>(tiles) * (offx + cx) / nwg);
   const int full_x = (hi - lo) / cx, rem_x = (hi - lo) - full_x * cx;
-  const bool halves = kHalves && full_x >= 1 && rem_x > 0 && 2 * rem_x <= cx;
+  // (no half units where the epilogue finishes a LayerNorm: its tiles need every wave)
+  const bool halves = LNF != 3 && kHalves && full_x >= 1 && rem_x > 0 && 2 * rem_x <= cx;
   const int my_full = halves ? full_x : (xk < hi - lo ? (hi - lo - xk + cx - 1) / cx : 0);
-  const int my_units = my_full + (halves && xk < 2 * rem_x ? 1 : 0);
+  // (a launch whose epilogue finishes a LayerNorm has one tile per workgroup:
+  // the launcher checks that the grid covers every tile)
+  const int my_units = LNF == 3 ? min(my_full, 1) : my_full + (halves && xk < 2 * rem_x ? 1 : 0);
   if (my_units == 0) return;
   const int total = my_units * nk;
   // unit u of this workgroup: its tile (m, n) and half (-1: the whole tile)
@@ -1274,7 +1510,7 @@ void gemm_bf16_pers_kernel(GemmArgs g0) {
       }
     }
     const int m0 = tm * BM + (th < 0 ? 0 : (BM / 2) * th);
-    static_assert(LNF == 0 || (LNF == 1 && EPI != EPI_RESID) || (LNF == 2 && EPI == EPI_RESID),
+    static_assert(LNF == 0 || (LNF == 1 && EPI != EPI_RESID) || (LNF >= 2 && EPI == EPI_RESID),
                   "folded LayerNorm roles");
     // RoPE units: positions of the unit's 256 rows to LDS (waves 0-3, 64 rows
     // each), copied during the first K step and read at the unit's end
@@ -1460,6 +1696,11 @@ void gemm_bf16_pers_kernel(GemmArgs g0) {
           reinterpret_cast<float*>(fold_lds) + WGN * BM);
       continue;
     }
+    if constexpr (LNF == 3) {  // and the next LayerNorm, finished with the panel's other tiles
+      resid_rln_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, WGN>(g, acc, m0, tm, tn, wme, wne, l32e, hbe,
+                                                             wave_s * 64 + lane_e, fold_lds);
+      continue;
+    }
     if constexpr (kSwap)
       pers_epilogue<BM, BN, TT::WM, TT::WN, TI, TJ, EPI, OutT>(g, acc, m0, tn, wme, wne, l32e, hbe);
     else
@@ -1485,7 +1726,10 @@ void launch_pers_kernel(const GemmArgs& g, hipStream_t st) {
   // (+ 1 KB of row positions for the RoPE epilogue, + a folded LayerNorm's
   // tables: the consumer's moments copy (8 bytes per row and block) and row
   // table (16 + 4 bytes per row), or the producer's WGN + 1 floats per row)
-  constexpr int fold = LNF == 1 ? BM * (kLnMaxBlocks * 8 + 20) : LNF == 2 ? 4 * (WGN + 1) * BM : 0;
+  constexpr int fold = LNF == 1   ? BM * (kLnMaxBlocks * 8 + 20)
+                       : LNF == 2 ? 4 * (WGN + 1) * BM
+                       : LNF == 3 ? 4 * (WGN + 3) * BM + 16
+                                  : 0;
   constexpr int lds = NS * PTile<BM, BN, WGM, WGN, NS, BK, W8>::STAGE_BYTES + 1024 + fold;
   static_assert(lds <= 160 * 1024, "LDS");
   auto kern = gemm_bf16_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI, OutT, LNF>;
@@ -1501,6 +1745,9 @@ void launch_pers_kernel(const GemmArgs& g, hipStream_t st) {
   require(tiles < (int64_t{1} << 30), "gemm: too many tiles");
   constexpr int occ = pers_occupancy<BM, BN, WGM, WGN, NS, BK, W8>();
   const int grid = static_cast<int>(std::min<int64_t>(tiles, int64_t{occ} * num_cus()));
+  // a tile of a LayerNorm-finishing launch waits for its panel's other tiles:
+  // each of them needs a workgroup of its own (one round)
+  if constexpr (LNF == 3) require(grid == tiles, "gemm: the residual epilogue's LayerNorm needs a workgroup per tile");
   kern<<<grid, 64 * WGM * WGN, lds, st>>>(g);
 }
 
@@ -1517,6 +1764,13 @@ void launch_pers(const GemmArgs& g, hipStream_t st) {
          : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_STORE, float, 0>(g, st);
       break;
     case EPI_RESID:
+      if constexpr (!W8 && BM == 256 && BN == 256 && WGM == 4 && WGN == 4) {
+        if (g.rln_y) {
+          launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_RESID, float, 3>(g, st);
+          break;
+        }
+      }
+      require(!g.rln_y, "gemm: the residual epilogue's LayerNorm needs the bf16 256 x 256 tile");
       g.ln_y ? launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_RESID, float, 2>(g, st)
              : launch_pers_kernel<BM, BN, WGM, WGN, NS, BK, W8, EPI_RESID, float, 0>(g, st);
       break;
@@ -1848,6 +2102,16 @@ bool gemm_takes_ln_fold(const GemmArgs& g) {
   return g.w_dtype == DT_BF16 && mfma_ok(g) && g.M >= 4096 && pers_ok(g);  // launch_mfma's first choice
 }
 
+bool gemm_takes_rln(const GemmArgs& g) {
+  if (g.epi != EPI_RESID || g.w_dtype != DT_BF16 || g.M <= 0 || g.N % kLnBlock != 0 ||
+      g.N / kLnBlock > kLnMaxBlocks || !g.A || !g.W || !g.X)
+    return false;
+  if (!(mfma_ok(g) && g.M >= 4096 && pers_ok(g))) return false;  // launch_mfma's persistent path
+  // one round: every tile a workgroup of its own, all resident at once
+  const int64_t tiles = static_cast<int64_t>(g.N / kLnBlock) * ((g.M + 255) / 256);
+  return tiles <= static_cast<int64_t>(pers_occupancy<SJH_GEMM_PERS, false>()) * num_cus();
+}
+
 int launch_gemm_resid_partials(const GemmArgs& g0, hipStream_t st) {
   if (g0.epi != EPI_RESID || g0.M <= 0 || g0.M > SJH_SPLITK_MAX_M || g0.N <= 0 || g0.K <= 0 || !g0.partial ||
       !g0.A || !g0.W || !g0.X || g0.lda < g0.K || g0.ldw < g0.K || g0.ldx < g0.N || !mfma_ok(g0))
@@ -1881,6 +2145,13 @@ void launch_gemm(const GemmArgs& g, hipStream_t st) {
       break;
     default:
       fail("gemm: unknown epilogue");
+  }
+  if (g.rln_y) {
+    require(gemm_takes_rln(g), "gemm: the residual epilogue finishes a LayerNorm only on one round of 256 x 256 "
+                               "bf16 tiles with N a multiple of 256 up to 1024");
+    require(g.rln_w && g.rln_mom && g.rln_sync && g.rln_ldy >= g.N && g.rln_spin > 0 && g.rln_eps > 0.f &&
+                !g.ln_y && !g.ln_stats_in,
+            "gemm: the residual epilogue's LayerNorm needs weights, moments, sync ints, a poll bound and ldy >= N");
   }
   if (g.ln_y || g.ln_stats_in) {
     require(gemm_takes_ln_fold(g),

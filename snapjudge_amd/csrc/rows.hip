@@ -284,24 +284,78 @@ __global__ __launch_bounds__(64 * WPB) void ln_vec_kernel(LnArgs a) {
   }
   float inv = 1.f, fmean = 0.f;
   if (a.normalize) {
-    const double x0 = static_cast<double>(__builtin_bit_cast(
-        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0][0]))));
-    double s1 = 0.0, s2 = 0.0;
+    if constexpr (FULL) {
+      // D = 256 NV: the 256-column block statistics of sjh_common.hpp
+      // (ln_block_combine), the residual epilogue's arithmetic bit for bit.
+      // Block b is chunk 64 b + lane: columns 256 b + 4 lane + [0, 4), so the
+      // tree's column distances 32, 16, 8, 4 are lane distances 8, 4, 2, 1
+      // inside each 16-lane DPP row (one row per 64-column group) and 2, 1
+      // are inside the lane.  Each level's sums gather in the upper lane of
+      // its pairs (row_shr), so lane 15 of row g ends with group g's sum; the
+      // groups combine as (g0 + g1) + (g2 + g3) through row broadcasts into
+      // lane 63.
+      float x0b[kLnStatMaxBlocks] = {}, sb[kLnStatMaxBlocks] = {}, qb[kLnStatMaxBlocks] = {};
+      auto shr = [](float x, auto ctrl_tag) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                    decltype(ctrl_tag)::value, 0xf, 0xf, false));
+      };
+      using Shr4 = std::integral_constant<int, 0x114>;
+      using Shr2 = std::integral_constant<int, 0x112>;
+      using Shr1 = std::integral_constant<int, 0x111>;
+      auto tree = [&](float (&t4)[4]) {  // t4: level 1 done (lane distance 8)
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (FULL || lane + 64 * i < nch)
+        for (int k = 0; k < 4; ++k) t4[k] = t4[k] + shr(t4[k], Shr4{});
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const double d = static_cast<double>(v[i][k]) - x0;
-          s1 += d;
-          s2 += d * d;
-        }
-    wave_sum2(s1, s2);
-    const double dm = s1 / static_cast<double>(D);
-    const double mean = x0 + dm;
-    const double var = fmax(s2 / static_cast<double>(D) - dm * dm, 0.0);
-    inv = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
-    fmean = static_cast<float>(mean);
+        for (int k = 0; k < 4; ++k) t4[k] = t4[k] + shr(t4[k], Shr2{});
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t4[k] = t4[k] + shr(t4[k], Shr1{});
+        float g = (t4[0] + t4[2]) + (t4[1] + t4[3]);
+        g = g + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, g), 0x142, 0xa,
+                                                                        0xf, false));  // row_bcast:15
+        g = g + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, g), 0x143, 0xc,
+                                                                        0xf, false));  // row_bcast:31
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g), 63));
+      };
+      using Shr8 = std::integral_constant<int, 0x118>;
+#pragma unroll
+      for (int b = 0; b < NV; ++b) {
+        const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[b][0])));
+        float d[4], t4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d[k] = v[b][k] - x0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t4[k] = d[k] + shr(d[k], Shr8{});  // columns k + 32 (own), k (shifted)
+        const float sm = tree(t4) * (1.0f / kLnStatBlock);
+        float e[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) e[k] = d[k] - sm;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t4[k] = ln_pair_sq(shr(e[k], Shr8{}), e[k]);
+        x0b[b] = x0;
+        sb[b] = sm;
+        qb[b] = tree(t4);
+      }
+      ln_block_combine(x0b, sb, qb, NV, a.eps, fmean, inv);
+    } else {
+      const double x0 = static_cast<double>(__builtin_bit_cast(
+          float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0][0]))));
+      double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (FULL || lane + 64 * i < nch)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const double d = static_cast<double>(v[i][k]) - x0;
+            s1 += d;
+            s2 += d * d;
+          }
+      wave_sum2(s1, s2);
+      const double dm = s1 / static_cast<double>(D);
+      const double mean = x0 + dm;
+      const double var = fmax(s2 / static_cast<double>(D) - dm * dm, 0.0);
+      inv = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
+      fmean = static_cast<float>(mean);
+    }
   }
   float* xo = a.x_out ? a.x_out + static_cast<int64_t>(r) * a.ld_x : nullptr;
   OutT* yo = a.y_out ? static_cast<OutT*>(a.y_out) + static_cast<int64_t>(r) * a.ld_y : nullptr;
@@ -312,11 +366,7 @@ __global__ __launch_bounds__(64 * WPB) void ln_vec_kernel(LnArgs a) {
     float y[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
     if (a.normalize) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        y[k] = (y[k] - fmean) * inv;
-        if (a.w) y[k] = y[k] * w[i][k];
-        if (a.b) y[k] = y[k] + b[i][k];
-      }
+      for (int k = 0; k < 4; ++k) y[k] = ln_apply(y[k], fmean, inv, w[i][k], b[i][k], a.b != nullptr);
     }
     if (xo) Vec4<float>::store(xo + 4 * c, y);
     if (yo) Vec4<OutT>::store(yo + 4 * c, y);

@@ -148,6 +148,63 @@ __device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
                                    0, 0);
 }
 
+// ---- LayerNorm statistics (src/tensor.cpp:54-79) -------------------------
+// Shared by the standalone LayerNorm and the residual GEMM epilogue that
+// finishes one, so that both give the same bits.  A row of D = 256 nb
+// columns is taken in 256-column blocks.  Per block, d = x - x0 (x0 the
+// block's first value) is summed over a fixed pairwise tree -- columns k and
+// k + 32 of each 64-column group first, then the partial sums at column
+// distance 16, 8, 4, 2 and 1, then the four groups as (g0 + g1) + (g2 + g3)
+// -- and s = sum /
+// 256; the squares of e = d - s go through the same tree, its first level as
+// fma(e[k + 32], e[k + 32], e[k] * e[k]).  The blocks combine in double: the
+// block means x0 + s, the row mean, and the pooled sum of squared deviations
+// (Chan et al.), giving the population variance; the mean and the inverse
+// std are then rounded to float and y = (x - mean) * inv * w (+ b) in float,
+// as the reference computes them.  The shift keeps the fp32 sums exact to
+// the rows' spread however large their offset.
+constexpr int kLnStatBlock = 256;
+constexpr int kLnStatMaxBlocks = 4;
+
+// First level of the squares' tree: e_lo = e[k], e_hi = e[k + 32].
+__device__ __forceinline__ float ln_pair_sq(float e_lo, float e_hi) {
+#pragma clang fp contract(off)
+  return __builtin_fmaf(e_hi, e_hi, e_lo * e_lo);
+}
+
+// Row statistics from the nb blocks' (x0, s, q): mean and inverse std.
+__device__ __forceinline__ void ln_block_combine(const float (&x0)[kLnStatMaxBlocks], const float (&s)[kLnStatMaxBlocks],
+                                                 const float (&q)[kLnStatMaxBlocks], int nb, float eps,
+                                                 float& fmean, float& finv) {
+  double mb[kLnStatMaxBlocks], sum = 0.0;
+#pragma unroll
+  for (int b = 0; b < kLnStatMaxBlocks; ++b)
+    if (b < nb) {
+      mb[b] = static_cast<double>(x0[b]) + static_cast<double>(s[b]);
+      sum += mb[b];
+    }
+  const double mean = sum / nb;
+  double m2 = 0.0;
+#pragma unroll
+  for (int b = 0; b < kLnStatMaxBlocks; ++b)
+    if (b < nb) {
+      const double dm = mb[b] - mean;
+      m2 += static_cast<double>(q[b]) + static_cast<double>(kLnStatBlock) * dm * dm;
+    }
+  const double var = m2 / (static_cast<double>(kLnStatBlock) * nb);
+  fmean = static_cast<float>(mean);
+  finv = static_cast<float>(1.0 / sqrt(var + static_cast<double>(eps)));
+}
+
+// y = (x - mean) * inv * w (+ b), in this order and unfused.
+__device__ __forceinline__ float ln_apply(float x, float fmean, float finv, float w, float b, bool has_b) {
+#pragma clang fp contract(off)
+  float y = (x - fmean) * finv;
+  y = y * w;
+  if (has_b) y = y + b;
+  return y;
+}
+
 // 64-lane wavefront reductions via DPP-backed shuffles.
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {

@@ -87,7 +87,26 @@ struct GemmArgs {
   const uint16_t* ln_c1 = nullptr;      // bf16 [n_w][8], blocks past K / kLnBlock zero
   const float* ln_c2 = nullptr;         // [n_w] or null (an unbiased norm)
   float ln_eps = 1e-5f;
+  // The LayerNorm that reads the residual stream next, finished by the
+  // residual epilogue itself (EPI_RESID with rln_y; gemm_takes_rln): besides
+  // X += acc (+ bias) it writes rln_y[m][c] = bf16(LN(x)[c]) (row stride
+  // rln_ldy) with weights rln_w, optional bias rln_b and rln_eps, as
+  // launch_ln does, bit for bit (sjh_common.hpp's LayerNorm statistics).
+  // The N / 256 tiles of a 256-row panel exchange their rows' 256-column
+  // block moments through rln_mom (M x N/256 x 4 floats) and count
+  // themselves in through rln_sync (8 ints per panel, zero before the launch,
+  // zero again after it); a tile waits at most rln_spin polls for the others.
+  void* rln_y = nullptr;
+  int64_t rln_ldy = 0;
+  const float* rln_w = nullptr;
+  const float* rln_b = nullptr;
+  float rln_eps = 1e-5f;
+  float* rln_mom = nullptr;
+  int* rln_sync = nullptr;
+  int rln_spin = 0;
 };
+// Sync ints per 256-row panel of GemmArgs::rln_sync.
+constexpr int kRlnSyncInts = 8;
 constexpr int kLnBlock = 256;
 // The engine does not take the folded path (see Engine::stage_weights).
 constexpr bool kLnFoldEnabled = false;
@@ -103,6 +122,11 @@ bool gemm_takes_ln_fold(const GemmArgs& g);
 void launch_ln_fold_consts(const void* W, int w_dtype, const float* w_scale, int n_w, int K,
                            const float* ln_w, const float* ln_b, uint16_t* c1, float* c2,
                            hipStream_t st);
+// Whether the residual epilogue can finish the next LayerNorm for these
+// arguments (GemmArgs::rln_y): the persistent bf16 kernel, N a multiple of 256
+// up to 1024, and at most one tile per workgroup, so that all of a panel's
+// tiles run at once.
+bool gemm_takes_rln(const GemmArgs& g);
 // Short batches (M <= 256) of a residual GEMM (EPI_RESID, bf16 MFMA path):
 // launches only the split-K product into g.partial and returns the number of
 // splits S >= 2; the caller then adds the splits with the layer norm that

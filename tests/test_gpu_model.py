@@ -240,6 +240,71 @@ def test_folded_layer_norm_under_large_row_offsets(orc, offset):
     m.close()
 
 
+@pytest.mark.parametrize("offset", ["none", "row", "block"])
+def test_residual_epilogue_layer_norm(orc, offset):
+    # On one round of persistent 256 x 256 tiles (T >= 4096, at most 256
+    # tiles) the residual GEMMs' epilogues also write the LayerNorm that reads
+    # the residual stream next: the tiles of a 256-row panel publish their
+    # rows' 256-column moments and each normalises its own block once the
+    # panel's other tiles have arrived.  Checked against the standalone
+    # LayerNorm launches (fuse_ln=0, bit for bit) and the oracle on sampled rows, with
+    # large offsets on the residual stream: the same on every column of a row
+    # ("row", ~100x the spread; the LayerNorm removes it) or different per
+    # 256-column block ("block").  Two runs give the same bits, and so does
+    # the path of tiles that give up waiting (fuse_ln=2: one poll, the panel's
+    # last tile normalises their blocks from X), and so do the standalone
+    # LayerNorm launches (the same statistics in the same order).
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg2"], num_hidden_layers=2), seed=26)
+    cfg = synth.flat_cfg(rl, enc)
+    D, F = cfg["hidden_size"], cfg["intermediate_size"]
+    if offset != "none":
+        rng = np.random.default_rng(27)
+        u = rng.standard_normal(F).astype(np.float32)
+        if offset == "row":
+            v = np.full(D, 20.0, np.float32)
+        else:
+            v = np.repeat(np.array([25.0, -20.0, 5.0], np.float32), D // 3)
+        for i in range(cfg["num_hidden_layers"]):
+            k = f"encoder.layers.{i}.mlp.Wo.weight"
+            w[k] = synth.bf16_round(w[k] + np.outer(v, u).astype(np.float32) / np.sqrt(F))
+    ids, mask, lens = synth.make_batch(12, 480, 380, 480, cfg["vocab_size"], seed=28)
+    T = int(lens.sum())
+    assert 4096 <= T and 3 * ((T + 255) // 256) <= 256
+    print(f"rln {offset}: T={T}", flush=True)
+    fused = sj.Model(w, cfg, precision=BF16)
+    h1 = fused.encode(ids, mask)
+    h2 = fused.encode(ids, mask)
+    assert np.array_equal(h1, h2)
+    fused.close()
+    gave_up = sj.Model(w, cfg, precision=BF16, fuse_ln=2)
+    hg = gave_up.encode(ids, mask)
+    gave_up.close()
+    print(f"rln {offset}: one-poll path identical: {np.array_equal(hg, h1)}", flush=True)
+    assert np.array_equal(hg, h1)
+    plain = sj.Model(w, cfg, precision=BF16, fuse_ln=0)
+    hp = plain.encode(ids, mask)
+    plain.close()
+    # the standalone LayerNorm computes the same statistics in the same order
+    print(f"rln {offset}: fused vs standalone max|d|={valid_err(h1, hp, mask):.3g}", flush=True)
+    assert np.array_equal(h1, hp)
+    om = orc.model(w, cfg)
+    for b in (int(np.argmin(lens)), int(np.argmax(lens))):
+        n = int(lens[b])
+        ref = om.encode(ids[b:b + 1, :n], mask[b:b + 1, :n])[0]
+        err = float(np.abs(h1[b, :n] - ref).max())
+        perr = float(np.abs(hp[b, :n] - ref).max())
+        print(f"rln {offset}: row {b} n={n} max|d|={err:.3g} (standalone {perr:.3g})", flush=True)
+        if offset == "block":
+            # Per-block offsets survive the LayerNorm as block-wise offsets of
+            # its output; through QKV they give large logits whose softmax
+            # turns on bf16 roundings, so both bf16 paths leave the fp32
+            # oracle by ~0.4 here.  The fused path is held to the standalone
+            # path's accuracy.
+            assert err <= 1.25 * perr + 1e-3
+        else:
+            assert err <= TOL[BF16] and perr <= TOL[BF16]
+
+
 def test_more_than_256_sequences(orc):
     # More than 256 sequences: the sequence table, with the query-block prefix
     # that the attention work list is cut from, is filled on the host instead
