@@ -710,7 +710,11 @@ __device__ __forceinline__ void resid_rln_epilogue(const GemmArgs& g, f32x16_t (
   auto rowof = [&](int i, int e) { return i * 32 + 8 * (e >> 2) + (e & 3) + 4 * hb; };
 
   // 1) X += acc + bias, the sum x kept in acc; the X reads of a group of 8
-  //    rows go out before the first add (as in the plain residual epilogue)
+  //    rows go out before the first add (as in the plain residual epilogue).
+  //    The waves that publish the moments (threads tid < BM) store their X
+  //    after the arrival (3), so that their wait before it covers the moment
+  //    stores only; the other waves store theirs here.
+  const bool publisher = tid < BM;  // uniform per wave
   float bv[TJ];
 #pragma unroll
   for (int j = 0; j < TJ; ++j) bv[j] = g.bias ? g.bias[c0 + j * 32 + l32] : 0.f;
@@ -734,7 +738,7 @@ __device__ __forceinline__ void resid_rln_epilogue(const GemmArgs& g, f32x16_t (
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
           acc[i][j][e0 + e] = xv[e][j] + (acc[i][j][e0 + e] + bv[j]);
-          if (r < rows_in) *reinterpret_cast<float*>(xr + j * 128) = acc[i][j][e0 + e];
+          if (!publisher && r < rows_in) *reinterpret_cast<float*>(xr + j * 128) = acc[i][j][e0 + e];
         }
       }
     }
@@ -791,11 +795,28 @@ __device__ __forceinline__ void resid_rln_epilogue(const GemmArgs& g, f32x16_t (
     __hip_atomic_store(p + 1, mu[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(p + 2, q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  wait_vm_all();  // this thread's X and moment stores have completed
+  wait_vm_all();  // this thread's X or moment stores have completed
   __syncthreads();
 
-  // 3) count the tile in (its X stores and moment stores have completed)
+  // 3) count the tile in (its moment stores have completed), then the
+  //    publishers' X stores
   if (tid == 0) __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (publisher) {
+    // (the lane's offset recomputed here, so that no address of step 1 is
+    // held through the statistics)
+    const int ln = lane_id_here(), hbp = ln >> 5;
+    const uint32_t lop = static_cast<uint32_t>(ln & 31) * 4;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rb = i * 32 + 8 * (e >> 2) + (e & 3);  // the row less 4 hb
+        char* xr = xw + static_cast<uint32_t>((rb + 4 * hbp) * ld4 + lop);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          if (rb + 4 * hbp < rows_in) *reinterpret_cast<float*>(xr + j * 128) = acc[i][j][e];
+      }
+  }
   if (tid == 0) {
     int n = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int it = 0; n < nb && it < g.rln_spin; ++it) {
