@@ -131,6 +131,12 @@ __device__ __forceinline__ int64_t mfma_w_row(const GemmArgs& g, int tile_n, int
     int o = tile_n * (BN / 2) + wn * half + (within < half ? within : within - half);
     o = o < g.N ? o : g.N - 1;
     return within < half ? o : static_cast<int64_t>(g.N) + o;
+  } else if constexpr (EPI == EPI_ROPE && BN == 32) {
+    // 32-column RoPE tiles (head_dim 64): tile_n = 2 h + c takes dims
+    // 16 c + [0, 16) of head h (rows i < 16) and their rotation partners 32
+    // higher (rows i >= 16), so each pair meets in one tile
+    const int n = (tile_n >> 1) * 64 + (tile_n & 1) * 16 + (i & 15) + (i & 16) * 2;
+    return n < g.N ? n : g.N - 1;
   } else {
     const int n = tile_n * BN + i;
     return n < g.N ? n : g.N - 1;
@@ -251,6 +257,46 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, f32x16_t (&acc)
       body(std::false_type{});
     else
       body(std::true_type{});
+  } else if constexpr (EPI == EPI_ROPE && BN == 32) {
+    // 32-column tiles (see mfma_w_row): lane c < 16 holds dim d = 16 (tile_n
+    // & 1) + c of head tile_n >> 1, lane c + 16 dim d + 32; each takes its
+    // partner by a lane swap and writes its own output column.  A group of
+    // 16 rows per lane gathers its positions, then its table entries.
+    static_assert(WN == 32 && TJ == 1 && TI == 1, "one 32 x 32 block per wave");
+    const bool hi = l32 >= 16;
+    const int col = (tile_n >> 1) * 64 + (tile_n & 1) * 16 + (l32 & 15) + (hi ? 32 : 0);
+    const int d = (tile_n & 1) * 16 + (l32 & 15);
+    const bool rot = (tile_n >> 1) * 64 < 2 * g.rope_dim, qh = (tile_n >> 1) * 64 < g.rope_dim;  // uniform
+    OutT* out = static_cast<OutT*>(g.out);
+    float cs[16], sn[16];
+    if (rot) {
+      int p[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) p[e] = g.pos[min(row_base + 8 * (e >> 2) + (e & 3), g.M - 1)];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t tb = static_cast<int64_t>(min(max(p[e], 0), g.rope_rows - 1)) * 32 + d;
+        cs[e] = g.rope_cos[tb];
+        sn[e] = g.rope_sin[tb];
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        consume(cs[e]);
+        consume(sn[e]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float own = acc[0][0][e];
+      const float partner = swap16(own, hi);  // every lane takes part
+      const int m = row_base + 8 * (e >> 2) + (e & 3);
+      float v = own;
+      if (rot) {
+        v = hi ? rope_hi(partner, own, cs[e], sn[e]) : rope_lo(own, partner, cs[e], sn[e]);
+        if (qh) v *= g.q_scale;
+      }
+      if (m < g.M && col < g.N) store_f32(out + static_cast<int64_t>(m) * g.ldo + col, v);
+    }
   } else if constexpr (EPI == EPI_ROPE) {
     // head_dim 64 (checked by the launcher): block j holds dims [0, 32) of a
     // head when j is even and dims [32, 64) when odd; its partner is j ^ 1.
@@ -1875,9 +1921,9 @@ void launch_mfma_epi(const GemmArgs& g, hipStream_t st) {
 // products take 32-column tiles: a CU streams W at ~25 GB/s at most, so half
 // the W rows per workgroup on twice the workgroups shortens the K loop
 // (batch-1 Wi + GEGLU 10.2 -> 8.1 us per launch).  A GEGLU tile's input and
-// gate rows meet in the epilogue by a lane swap.  The RoPE product keeps
-// 64-column tiles: with its rotation pairs one per lane, its epilogue does
-// half the work per output (8.3 us against 9.0 with paired 32-column tiles).
+// gate rows meet in the epilogue by a lane swap, and so do the rotation
+// pairs of a RoPE tile (head_dim 64: 16 dims of a head and their partners 32
+// higher; batch-1 p50 1.084 -> 1.074 ms against 64-column RoPE tiles).
 #ifndef SJH_GEMM_SMALL32
 #define SJH_GEMM_SMALL32 64, 32, 2, 1, 4, 64
 #endif
@@ -1911,6 +1957,8 @@ void launch_mfma(const GemmArgs& g, hipStream_t st) {
     launch_mfma_tile<SJH_GEMM_SMALL32, EPI_GEGLU>(g, st);
   else if (g.M <= SJH_SMALL32_MAX_M && g.epi == EPI_STORE)
     launch_mfma_tile<SJH_GEMM_SMALL32, EPI_STORE>(g, st);
+  else if (g.M <= SJH_SMALL32_MAX_M && g.epi == EPI_ROPE && g.head_dim == 64 && g.N % 64 == 0)
+    launch_mfma_tile<SJH_GEMM_SMALL32, EPI_ROPE>(g, st);
   else
     launch_mfma_epi<SJH_GEMM_SMALL>(g, st);
 }

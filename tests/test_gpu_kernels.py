@@ -425,7 +425,7 @@ def test_gemm_tile_shape_invariance():
                         ("rope", 2304, 2304)):
         W = dev(rnd(rng, (nw, K), 0.05), torch.bfloat16)
         res = []
-        for M in (Mb, 1500, 300, Ms):  # persistent, 128x128, 64x64 and (GEGLU, store) 64x32 tiles
+        for M in (Mb, 1500, 300, Ms):  # persistent, 128x128, 64x64 and (GEGLU, store, RoPE) 64x32 tiles
             odt = torch.float32 if kind == "resid" else torch.bfloat16
             O = torch.zeros((M, n), dtype=odt, device="cuda")
             if kind == "store":
