@@ -305,6 +305,45 @@ def test_residual_epilogue_layer_norm(orc, offset):
             assert err <= TOL[BF16] and perr <= TOL[BF16]
 
 
+@pytest.mark.parametrize("D,H,F", [(512, 8, 768), (1024, 16, 2624)])
+def test_residual_epilogue_layer_norm_widths(orc, D, H, F):
+    # The residual epilogue that finishes the LayerNorm at two and four
+    # 256-column blocks per row (D = 512 and 1024; config 5's widths), with
+    # norm weights away from 1: bit for bit against the standalone LayerNorm
+    # (fuse_ln=0) and the give-up path (fuse_ln=2), rows against the oracle.
+    rl, enc, w = synth.make_model(hidden_size=D, num_hidden_layers=2, num_attention_heads=H,
+                                  intermediate_size=F, vocab_size=50368, store="BF16", seed=71)
+    cfg = synth.flat_cfg(rl, enc)
+    rng = np.random.default_rng(72)
+    for k in list(w):
+        if k.endswith(("attn_norm.weight", "mlp_norm.weight")):
+            w[k] = synth.bf16_round((1.0 + 0.2 * rng.standard_normal(D)).astype(np.float32))
+    ids, mask, lens = synth.make_batch(12, 480, 380, 480, cfg["vocab_size"], seed=73)
+    T = int(lens.sum())
+    assert 4096 <= T and (D // 256) * ((T + 255) // 256) <= 256
+    print(f"rln D={D}: T={T}", flush=True)
+    fused = sj.Model(w, cfg, precision=BF16)
+    h1 = fused.encode(ids, mask)
+    fused.close()
+    gave_up = sj.Model(w, cfg, precision=BF16, fuse_ln=2)
+    hg = gave_up.encode(ids, mask)
+    gave_up.close()
+    plain = sj.Model(w, cfg, precision=BF16, fuse_ln=0)
+    hp = plain.encode(ids, mask)
+    plain.close()
+    print(f"rln D={D}: one-poll identical {np.array_equal(hg, h1)}, standalone max|d|="
+          f"{valid_err(h1, hp, mask):.3g}", flush=True)
+    assert np.array_equal(hg, h1)
+    assert np.array_equal(hp, h1)
+    om = orc.model(w, cfg)
+    for b in (int(np.argmin(lens)), int(np.argmax(lens))):
+        n = int(lens[b])
+        ref = om.encode(ids[b:b + 1, :n], mask[b:b + 1, :n])[0]
+        err = float(np.abs(h1[b, :n] - ref).max())
+        print(f"rln D={D}: row {b} n={n} max|d|={err:.3g}", flush=True)
+        assert err <= TOL[BF16]
+
+
 def test_more_than_256_sequences(orc):
     # More than 256 sequences: the sequence table, with the query-block prefix
     # that the attention work list is cut from, is filled on the host instead
