@@ -469,6 +469,33 @@ def test_graph_replay_serves_a_shape_bucket():
     g_off.close()
 
 
+def test_graph_replay_with_residual_epilogue_layer_norm():
+    # Batches of one shape bucket at T > 4096 (one round of persistent
+    # residual tiles, whose epilogue finishes the LayerNorm through the row
+    # panels' sync ints) replay one captured graph: every launch leaves the
+    # ints at zero for the next replay.  Each result equals the launch-by-
+    # launch run with the standalone LayerNorm, bit for bit.
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS["cfg2"], num_hidden_layers=2), seed=48)
+    cfg = synth.flat_cfg(rl, enc)
+    g_on = sj.Model(w, cfg, precision=BF16, use_graphs=True)
+    g_off = sj.Model(w, cfg, precision=BF16, use_graphs=False, fuse_ln=0)
+    V = cfg["vocab_size"]
+    batches = [synth.batch_with_lens([370, 380, 360, 375, 365, 384, 372, 368, 377, 366, 371, 369], 384, V, seed=49),
+               synth.batch_with_lens([384, 300, 380, 350, 383, 376, 379, 381, 382, 330, 378, 380, 10], 384, V,
+                                     seed=50),
+               synth.batch_with_lens([350, 360, 340, 370, 345, 355, 365, 380, 384, 375, 362, 358], 384, V, seed=51)]
+    for ids, mask, lens in batches:
+        assert 4096 < int(lens.sum()) <= 4608 and 256 < lens.max() <= 384
+    for i, (ids, mask, lens) in enumerate(batches + [batches[0]]):
+        h = g_on.encode(ids, mask)
+        want = g_off.encode(ids, mask)
+        print(f"batch {i}: B={len(lens)} T={int(lens.sum())} graphs {g_on.graph_stats()}", flush=True)
+        assert np.array_equal(h, want)
+    assert g_on.graph_stats() == {"cached": 1, "captures": 1, "replays": 3}
+    g_on.close()
+    g_off.close()
+
+
 def test_graph_cache_eviction_waits_for_queued_launches():
     # More graphs than the cache holds (32), issued back to back with no host
     # synchronization: every capture past the 32nd evicts the least recently
