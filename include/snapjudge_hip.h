@@ -113,6 +113,11 @@ typedef struct sjh_options {
                          tile waits for its panel's other tiles for one poll only, so that
                          most tiles take the path of a tile that gave up waiting (the
                          results are the same bits as with 1; for tests) */
+  int32_t fuse_attn_wo; /* 1 (default): on short batches (at most 256 tokens, bf16, head_dim
+                         64) attention also multiplies each head's output by its slice of
+                         Wo, and the LayerNorm that reads the residual stream next adds the
+                         heads' partial products (no separate Wo launch); 0: Wo is a GEMM
+                         launch of its own */
 } sjh_options;
 
 typedef struct sjh_model sjh_model;

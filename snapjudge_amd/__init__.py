@@ -56,7 +56,8 @@ class ModelDesc(C.Structure):
 
 class Options(C.Structure):
     _fields_ = [("precision", C.c_int32), ("max_len", C.c_int32), ("use_graphs", C.c_int32),
-                ("pad_rows", C.c_int32), ("device", C.c_int32), ("fuse_ln", C.c_int32)]
+                ("pad_rows", C.c_int32), ("device", C.c_int32), ("fuse_ln", C.c_int32),
+                ("fuse_attn_wo", C.c_int32)]
 
 
 # Every symbol include/snapjudge_hip.h declares, with its ctypes signature.
@@ -185,7 +186,7 @@ class Model:
 
     def __init__(self, weights: "dict", cfg: "dict", precision: int = SJH_PREC_BF16,
                  max_len: int = 0, use_graphs: bool = True, pad_rows: bool = False,
-                 device: int = 0, fuse_ln: int = 1):
+                 device: int = 0, fuse_ln: int = 1, fuse_attn_wo: int = 1):
         self._keep = []
         w = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in weights.items()}
         self._keep.append(w)
@@ -234,7 +235,7 @@ class Model:
         d.act_w1, d.act_b1 = _ptr(w["act_head.0.weight"]), _ptr(w["act_head.0.bias"])
         d.act_w2, d.act_b2 = _ptr(w["act_head.2.weight"]), _ptr(w["act_head.2.bias"])
         opt = Options(precision, max_len, 1 if use_graphs else 0, 1 if pad_rows else 0, device,
-                      int(fuse_ln))
+                      int(fuse_ln), int(fuse_attn_wo))
         h = C.c_void_p()
         check(lib().sjh_model_create(C.byref(d), C.byref(opt), C.byref(h)))
         self._h = h
@@ -246,13 +247,13 @@ class Model:
     @classmethod
     def load(cls, path: str, precision: int = SJH_PREC_BF16, max_len: int = 0,
              use_graphs: bool = True, pad_rows: bool = False, device: int = 0,
-             fuse_ln: int = 1) -> "Model":
+             fuse_ln: int = 1, fuse_attn_wo: int = 1) -> "Model":
         """A checkpoint directory loaded straight to the device (sjh_model_load):
         a DecisionModel (rl_agent_config.json + encoder/config.json) or an
         SjModel (sj_config.json), with model.safetensors."""
         self = cls.__new__(cls)
         opt = Options(precision, max_len, 1 if use_graphs else 0, 1 if pad_rows else 0, device,
-                      int(fuse_ln))
+                      int(fuse_ln), int(fuse_attn_wo))
         h = C.c_void_p()
         check(lib().sjh_model_load(os.fsencode(path), C.byref(opt), C.byref(h)))
         self._h = h

@@ -141,11 +141,30 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 // start at row0 (q0 < qlen).  half 0: all keys; 1: keys [0, mid), 2: keys
 // [mid, klen) with mid = klen / 2 rounded up to a whole tile (full attention
 // only), the unnormalised result going to part (kAttnPartFloats floats).
-template <bool PRE>
+// WO: the output projection folded in (AttnArgs::wo): the workgroup's
+// kAttnWoCols rows of Wo (grid y) go to LDS at kWoLds while the item runs,
+// and the item writes its partial product instead of O.
+constexpr int kWoLds = kNS * kStage + 1024;
+template <bool PRE, bool WO = false>
 __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t row0, int qlen, int klen,
                                           int h, int q0, int half = 0, float* part = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hb = lane >> 5;
+  const int n0 = WO ? static_cast<int>(blockIdx.y) * kAttnWoCols : 0;
+  if constexpr (WO) {
+    // rows n0 + [0, kAttnWoCols) of Wo, columns 64 h + [0, 64): 128-byte
+    // rows swizzled as the K/V tiles (kv_off), groups of 8 rows per load,
+    // wave w moving groups w, w + 4, ...
+    const bf16_t* Wo = static_cast<const bf16_t*>(a.wo) + static_cast<int64_t>(n0) * a.ld_wo + h * 64;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+    for (int i = 0; i < kAttnWoCols / 32; ++i) {
+      const int grp = wave_u + 4 * i;
+      const int r = 8 * grp + (lane >> 3);
+      load_lds16(Wo + static_cast<int64_t>(r) * a.ld_wo + (((lane & 7) ^ kv_swz(r)) << 3),
+                 smem + kWoLds + grp * 1024);
+    }
+  }
 
   const bf16_t* Q = static_cast<const bf16_t*>(a.q) + h * 64;
   const bf16_t* K = static_cast<const bf16_t*>(a.k) + h * 64;
@@ -511,6 +530,50 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, char* smem, int64_t
     return;
   }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if constexpr (WO) {
+    // P[q][n] = sum_d O[q][d] Wo[n0 + n][64 h + d] by v_mfma_f32_32x32x16_bf16
+    // with A = Wo rows, B = O^T: the B fragment of K step (db, sub) is the
+    // accumulator o[db][8 sub + t] itself (lane (q, hb) holds dims 8 (e / 4)
+    // + 4 hb + e % 4 of its 32-dim block), so its k slot 8 hb + t stands for
+    // dim 16 sub + 4 hb + t (t < 4) or 16 sub + 8 + 4 hb + t - 4, and the A
+    // fragments are read in that order (two 8-byte reads).  O is rounded to
+    // bf16 after the 1 / l normalisation, as the O store does.
+    wait_vmcnt<0>();  // the Wo chunk (all else has landed)
+    __syncthreads();  // every wave's share of it
+    if (!wave_active) return;
+    bf16x8_t ob[2][2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) ob[db][sub][t] = static_cast<__bf16>(o[db][8 * sub + t] * inv);
+    const char* wl = smem + kWoLds;
+    float* P = a.wo_part + h * a.wo_part_stride + (row0 + min(qi, qlen - 1)) * a.wo_ld_part + n0 + 4 * hb;
+#pragma unroll
+    for (int nb = 0; nb < kAttnWoCols / 32; ++nb) {
+      f32x16_t d;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) d[e] = 0.f;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+          const int row = nb * 32 + l32, col = db * 32 + 16 * sub + 4 * hb;
+          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(wl + kv_off(row, col));
+          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(wl + kv_off(row, col + 8));
+          const bf16x8_t af = __builtin_bit_cast(bf16x8_t, (u32x4_t){lo[0], lo[1], hi[0], hi[1]});
+          d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, ob[db][sub], d, 0, 0, 0);
+        }
+      // lane (q, hb): columns nb * 32 + 8 g + 4 hb + [0, 4) of its query's row
+      if (qi < qlen) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4_t*>(P + nb * 32 + 8 * g) = (f32x4_t){d[4 * g], d[4 * g + 1], d[4 * g + 2], d[4 * g + 3]};
+      }
+    }
+    return;
+  }
   if (qi < qlen) {
     bf16_t* O = static_cast<bf16_t*>(a.o) + (row0 + qi) * a.ld_o + h * 64;
 #pragma unroll
@@ -572,6 +635,18 @@ __global__ __launch_bounds__(256, 3) void attn_bf16_mfma_kernel(AttnArgs a) {
   const int q0 = (kx % nblk) * kQ;
   if (q0 >= qlen) return;  // uniform over the workgroup
   attn_item<PRE>(a, smem, row0, qlen, klen, h, q0);
+}
+
+// The work list's items with the output projection folded in (AttnArgs::wo):
+// workgroup (slot, y) runs slot's item for Wo rows y * kAttnWoCols + [0,
+// kAttnWoCols).
+template <bool PRE>
+__global__ __launch_bounds__(256) void attn_wo_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kWoLds + kAttnWoCols * 128];
+  const int4 m = reinterpret_cast<const int4*>(a.items)[blockIdx.x];
+  if (m.y <= 0) return;  // an empty slot (uniform over the workgroup)
+  const int q0 = static_cast<int>(static_cast<uint32_t>(m.w) >> 16) * kQ;
+  attn_item<PRE, true>(a, smem, m.x, m.y, m.z, m.w & 0x3fff, q0);
 }
 
 // First rank of the key-split tail (Bb: none): the smallest rank z, at a
@@ -816,6 +891,20 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
       nwg = pairs8 * ((a.max_q + kQ - 1) / kQ);
     }
     require(nwg < (int64_t{1} << 31), "attention: too many workgroups");
+    if (a.wo) {
+      require(a.items && !a.part && a.wo_n > 0 && a.wo_n % kAttnWoCols == 0 && a.ld_wo >= 64 * int64_t{a.H} &&
+                  a.ld_wo % 8 == 0 && aligned16(a.wo) && a.wo_part && aligned16(a.wo_part) &&
+                  a.wo_ld_part >= a.wo_n && a.wo_ld_part % 4 == 0 && a.wo_part_stride % 4 == 0,
+              "attention: the folded output projection needs the work list without split items, bf16 Wo rows "
+              "of at least 64 H values, a multiple of 128 rows and 16-byte aligned partials");
+      const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(a.wo_n / kAttnWoCols));
+      if (a.q_log2_scaled)
+        attn_wo_kernel<true><<<grid, dim3(256), 0, st>>>(a);
+      else
+        attn_wo_kernel<false><<<grid, dim3(256), 0, st>>>(a);
+      check_launch("attn_wo");
+      return;
+    }
     if (a.q_log2_scaled)
       attn_bf16_mfma_kernel<true><<<dim3(static_cast<unsigned>(nwg)), dim3(256), 0, st>>>(a);
     else

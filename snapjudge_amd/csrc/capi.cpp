@@ -76,6 +76,7 @@ void sjh_default_options(sjh_options* opt) {
   opt->pad_rows = 0;
   opt->device = 0;
   opt->fuse_ln = 1;
+  opt->fuse_attn_wo = 1;
 }
 
 int sjh_model_create(const sjh_model_desc* desc, const sjh_options* opt, sjh_model** out) {

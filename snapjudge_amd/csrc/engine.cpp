@@ -234,6 +234,7 @@ Engine::Engine(const ModelSource& src, const sjh_options& o) {
   pad_rows_ = o.pad_rows != 0;
   rln_ = o.fuse_ln != 0;
   rln_spin_ = o.fuse_ln == 2 ? 1 : kRlnSpin;
+  attn_wo_ = o.fuse_attn_wo != 0;
 
   arch_ = src.arch;
   act_head_ = src.act_head;
@@ -922,6 +923,13 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
             "attention work list: workspace too small");
     launch_attn_items(si, Bb, H_, attn_slots, attn_split, w.attn_items, st);
   }
+  // short batches: attention folds the output projection in (AttnArgs::wo),
+  // each head's partial product going to the split-K workspace, and the
+  // LayerNorm that reads X next adds the H partials (LnArgs::parts), so no
+  // Wo launch runs
+  const bool attn_wo = attn_wo_ && attn_list && !attn_split && !w8_ && T <= 256 && D == 64 * H_ &&
+                       D % kAttnWoCols == 0 && D <= 1024 && w.partial &&
+                       static_cast<int64_t>(H_) * T * D <= w.partial_cap;
 
   // src/model.cpp:332-340: X = LN(emb[ids]); layer 0 reads X itself.  BERT
   // family (src/sj_model.cpp:220-237): X = LN(word[ids] + pos[position] ; w, b)
@@ -1088,10 +1096,18 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
         a.n_slots = attn_slots;
         if (attn_split) a.part = w.attn_part;
       }
+      if (attn_wo) {
+        a.wo = ly.wo.get();
+        a.ld_wo = D;
+        a.wo_n = D;
+        a.wo_part = w.partial;
+        a.wo_part_stride = static_cast<int64_t>(T) * D;
+        a.wo_ld_part = D;
+      }
       prof_begin(st);
       launch_attn(a, st);
       if (attn_split) launch_attn_merge(si, Bb, H_, attn_pairs, w.attn_part, O, D, st);
-      prof_end("attention", st);
+      prof_end(attn_wo ? "attention_wo" : "attention", st);
     }
     {  // X += O . Wo^T (src/model.cpp:389-391)
       GemmArgs g;
@@ -1123,7 +1139,17 @@ void Engine::enqueue_encoder(const BatchPlan& p, const Ws& w, const int32_t* d_i
       a.M = T;
       a.M_dev = T_dev;
       a.D = D;
-      if (fold) {
+      if (attn_wo) {  // attention wrote the heads' partials of O . Wo^T
+        LnArgs f = a;
+        f.parts = w.partial;
+        f.n_parts = H_;
+        f.part_stride = static_cast<int64_t>(T) * D;
+        f.ld_part = D;
+        f.part_bias = g.bias;
+        f.xio = X;
+        require(ln_takes_parts(f), "the layer norm after the folded output projection takes no partials");
+        ln("mlp_norm", f, st);
+      } else if (fold) {
         g.ln_y = Y;
         g.ln_w = ly.mlp_norm.as<float>();
         g.ln_stats_out = w.ln_stats;

@@ -242,6 +242,9 @@ class Engine {
   // where their tiles all run at once (sjh_options::fuse_ln)
   bool rln_ = false;
   int rln_spin_ = 0;  // GemmArgs::rln_spin
+  // short batches: attention folds the output projection in (AttnArgs::wo;
+  // sjh_options::fuse_attn_wo)
+  bool attn_wo_ = false;
   int arch_ = ARCH_MODERNBERT;  // ModernBERT (DecisionModel) or BERT (SjModel)
   int act_head_ = ACT_MLP;
   int head_ff_ = 0, head_act_ = 2;

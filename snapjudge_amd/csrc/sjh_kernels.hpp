@@ -219,7 +219,20 @@ struct AttnArgs {
   // Partials of the work list's key-split items (launch_attn_items with
   // split): kAttnPartFloats floats per half item, merged by launch_attn_merge.
   float* part = nullptr;
+  // Optional output projection folded in (bf16 head_dim-64 kernel with the
+  // work list, no split items): instead of o, item (head h, query block)
+  // writes its queries' O_h . Wo[:, 64h : 64h + 64]^T, fp32, to
+  // wo_part[h * wo_part_stride + row * wo_ld_part + n] for n < wo_n, so the
+  // H slices summed in head order (a LayerNorm with LnArgs::parts) give
+  // O . Wo^T.  Wo is bf16 [wo_n][ld_wo], wo_n a multiple of kAttnWoCols (the
+  // columns of one workgroup; grid y = wo_n / kAttnWoCols).
+  const void* wo = nullptr;
+  int64_t ld_wo = 0;
+  int wo_n = 0;
+  float* wo_part = nullptr;
+  int64_t wo_part_stride = 0, wo_ld_part = 0;
 };
+constexpr int kAttnWoCols = 128;
 void launch_attn(const AttnArgs& a, hipStream_t st);
 
 // Attention work list of a batch (AttnArgs::items): the (sequence, head,

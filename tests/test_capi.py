@@ -35,7 +35,7 @@ def test_version_and_default_options():
     assert lib.sjh_version() == 1
     o = sj.Options()
     lib.sjh_default_options(C.byref(o))
-    assert (o.precision, o.use_graphs, o.pad_rows, o.device, o.fuse_ln) == (sj.SJH_PREC_BF16, 1, 0, 0, 1)
+    assert (o.precision, o.use_graphs, o.pad_rows, o.device, o.fuse_ln, o.fuse_attn_wo) == (sj.SJH_PREC_BF16, 1, 0, 0, 1, 1)
 
 
 def test_null_arguments_are_rejected():

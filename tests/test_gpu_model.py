@@ -344,6 +344,42 @@ def test_residual_epilogue_layer_norm_widths(orc, D, H, F):
         assert err <= TOL[BF16]
 
 
+@pytest.mark.parametrize("preset,lens", [("cfg2", [128]), ("cfg2", [90, 70, 60]), ("cfg5", [128]),
+                                         ("cfg5", [200, 56])])
+def test_attention_folds_output_projection_on_short_batches(orc, preset, lens):
+    # Short batches (T <= 256): attention multiplies each head's output by its
+    # 64-column slice of Wo (one workgroup per 128 Wo rows) and the LayerNorm
+    # that reads X next adds the H partial products in head order, with no Wo
+    # launch.  One and two query blocks, D 768 and 1024, two layers (the
+    # second with an attention LayerNorm): repeated calls give the same bits,
+    # the result stays within the bf16 tolerance of the two-launch path
+    # (fuse_attn_wo=0: the sum over K runs in another order) and of the oracle
+    # on every row.
+    rl, enc, w = synth.make_model(**dict(synth.PRESETS[preset], num_hidden_layers=2), seed=81)
+    cfg = synth.flat_cfg(rl, enc)
+    ids, mask, lens = synth.batch_with_lens(np.array(lens), max(lens), cfg["vocab_size"], seed=82)
+    print(f"attention + Wo {preset}: T={int(lens.sum())}", flush=True)
+    fused = sj.Model(w, cfg, precision=BF16)
+    h1 = fused.encode(ids, mask)
+    h2 = fused.encode(ids, mask)
+    fused.close()
+    assert np.array_equal(h1, h2)
+    plain = sj.Model(w, cfg, precision=BF16, fuse_attn_wo=0)
+    hp = plain.encode(ids, mask)
+    plain.close()
+    d = valid_err(h1, hp, mask)
+    print(f"attention + Wo {preset}: against the two-launch path max|d|={d:.3g}", flush=True)
+    assert d <= TOL[BF16]
+    om = orc.model(w, cfg)
+    for b in range(len(lens)):
+        n = int(lens[b])
+        ref = om.encode(ids[b:b + 1, :n], mask[b:b + 1, :n])[0]
+        err = float(np.abs(h1[b, :n] - ref).max())
+        perr = float(np.abs(hp[b, :n] - ref).max())
+        print(f"attention + Wo {preset}: row {b} n={n} max|d|={err:.3g} (two launches {perr:.3g})", flush=True)
+        assert err <= TOL[BF16]
+
+
 def test_more_than_256_sequences(orc):
     # More than 256 sequences: the sequence table, with the query-block prefix
     # that the attention work list is cut from, is filled on the host instead
