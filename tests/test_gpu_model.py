@@ -345,7 +345,7 @@ def test_residual_epilogue_layer_norm_widths(orc, D, H, F):
 
 
 @pytest.mark.parametrize("preset,lens", [("cfg2", [128]), ("cfg2", [90, 70, 60]), ("cfg5", [128]),
-                                         ("cfg5", [200, 56])])
+                                         ("cfg5", [200, 56]), ("sliding", [200, 40])])
 def test_attention_folds_output_projection_on_short_batches(orc, preset, lens):
     # Short batches (T <= 256): attention multiplies each head's output by its
     # 64-column slice of Wo (one workgroup per 128 Wo rows) and the LayerNorm
@@ -355,7 +355,12 @@ def test_attention_folds_output_projection_on_short_batches(orc, preset, lens):
     # the result stays within the bf16 tolerance of the two-launch path
     # (fuse_attn_wo=0: the sum over K runs in another order) and of the oracle
     # on every row.
-    rl, enc, w = synth.make_model(**dict(synth.PRESETS[preset], num_hidden_layers=2), seed=81)
+    if preset == "sliding":  # a sliding-window layer (window 128) over a 200-token row
+        p = dict(synth.PRESETS["cfg2"], num_hidden_layers=2, layer_types=["sliding_attention", "full_attention"],
+                 local_attention=128)
+    else:
+        p = dict(synth.PRESETS[preset], num_hidden_layers=2)
+    rl, enc, w = synth.make_model(**p, seed=81)
     cfg = synth.flat_cfg(rl, enc)
     ids, mask, lens = synth.batch_with_lens(np.array(lens), max(lens), cfg["vocab_size"], seed=82)
     print(f"attention + Wo {preset}: T={int(lens.sum())}", flush=True)
