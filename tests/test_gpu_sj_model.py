@@ -66,6 +66,17 @@ def test_sj_model_768_wide(orc, tmp_path, prec):
           seed=104)
 
 
+@pytest.mark.parametrize("prec", [FP32, BF16])
+def test_sj_model_768_short_batch(orc, tmp_path, prec):
+    # at most 256 tokens: in bf16 the attention kernel folds the output
+    # projection in (the BERT family's queries are not pre-scaled, so its
+    # softmax scales the logits itself) and the layer norm adds the heads'
+    # partials with Wo's bias
+    cfg, w = synth.make_sj_model(hidden_size=768, num_layers=2, num_heads=12, vocab_size=3000,
+                                 max_positions=512, head_layers=1, store="BF16", seed=107)
+    check(orc, tmp_path, cfg, w, "BF16", prec, 2, 120, 60, 120, [(0, 5), (1, 4)], 5, seed=108)
+
+
 def test_sj_model_padded_rows(orc, tmp_path):
     cfg, w = synth.make_sj_model(hidden_size=64, num_layers=1, num_heads=2, vocab_size=200,
                                  max_positions=40, store="F32", seed=105)
